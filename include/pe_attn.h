@@ -1,0 +1,116 @@
+/*
+ * pe_attn.h — C ABI of the MI355X (gfx950) packed varlen attention library libpe_attn.so.
+ *
+ * Packed (padding-free) attention over flat [total_tokens, heads, head_dim] bf16 Q/K/V with
+ * int32 cu_seqlens boundaries, the hot path of packed-encoders. Every entry point takes plain
+ * pointers and sizes, never throws, and returns 0 or a negative PE_ATTN_E* status. Kernels are
+ * launched on the caller's stream with no host synchronisation and no device-to-host reads,
+ * so every entry point is safe inside HIP graph capture. The library allocates nothing: the
+ * one entry point that needs scratch memory takes a caller workspace.
+ *
+ * Semantics (identical for every entry point):
+ *   For each segment s with start = cu_seqlens[s], length L = cu_seqlens[s+1] - start, each
+ *   query row i < L of query head h reads keys j < L of kv head h / (n_heads_q / n_heads_kv):
+ *     allowed(i, j) = (window_left  < 0 || i - j <= window_left)
+ *                  && (window_right < 0 || j - i <= window_right)
+ *                  && (!causal || j <= i)
+ *     out[i] = sum_j softmax_j(scale * q_i . k_j over allowed j) * v_j
+ *   Arithmetic: fp32 scores and accumulation; probabilities are rounded to bf16 before the
+ *   P.V product and the normaliser is the fp32 sum of the unrounded probabilities; the output
+ *   is rounded to bf16. With a gate, out = bf16(bf16(out) * bf16(sigmoid(gate))).
+ *   Rows at or beyond cu_seqlens[n_seq] are never written. Empty segments are allowed.
+ *   Caller contract (not checked on device): cu_seqlens[0] = 0, non-decreasing,
+ *   cu_seqlens[n_seq] <= total_tokens, and max_seqlen >= every segment length.
+ */
+#ifndef PE_ATTN_H
+#define PE_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PE_ATTN_ABI_VERSION 1
+
+#define PE_ATTN_OK 0
+#define PE_ATTN_EINVAL (-1)       /* malformed arguments (maps to ValueError) */
+#define PE_ATTN_EUNSUPPORTED (-2) /* well-formed but outside the kernels' envelope */
+#define PE_ATTN_EWORKSPACE (-3)   /* workspace missing or too small */
+#define PE_ATTN_ELAUNCH (-4)      /* a kernel launch failed (maps to RuntimeError) */
+
+#define PE_ATTN_DTYPE_BF16 1
+
+typedef struct pe_attn_args {
+    uint32_t struct_size; /* sizeof(pe_attn_args): guards against a mismatched header */
+    int32_t dtype;        /* PE_ATTN_DTYPE_BF16 */
+    const void *q;        /* [total_tokens, n_heads_q,  head_dim] */
+    const void *k;        /* [total_tokens, n_heads_kv, head_dim] */
+    const void *v;        /* [total_tokens, n_heads_kv, head_dim] */
+    void *o;              /* [total_tokens, n_heads_q,  head_dim] (written) */
+    const void *gate;     /* optional [total_tokens, n_heads_q, head_dim]; NULL for none */
+    const int32_t *cu_seqlens; /* device [n_seq + 1] */
+    /* strides in elements; the head_dim stride is 1. 16-byte alignment of every row is
+       required: base pointers % 16 == 0 and token/head strides % 8 == 0. */
+    int64_t q_stride_token, q_stride_head;
+    int64_t k_stride_token, k_stride_head;
+    int64_t v_stride_token, v_stride_head;
+    int64_t o_stride_token, o_stride_head;
+    int64_t gate_stride_token, gate_stride_head;
+    int32_t n_seq;
+    int32_t total_tokens;
+    int32_t max_seqlen; /* host bound on every segment length */
+    int32_t n_heads_q;
+    int32_t n_heads_kv; /* divides n_heads_q */
+    int32_t head_dim;   /* 64, 128 or 256 */
+    float softmax_scale;
+    int32_t window_left;  /* -1: unbounded */
+    int32_t window_right; /* -1: unbounded */
+    int32_t causal;       /* 0 or 1; causal is window_right = 0 */
+    /* Per-segment routing: segments with length <= short_max run the LDS-resident short
+       kernel, longer ones the tiled MFMA kernel. 0 sends every segment to the tiled kernel;
+       -1 asks for the library's gfx950 default. At most 128 (64 for head_dim 256 is refused:
+       the short kernel covers head_dim <= 128). */
+    int32_t short_max;
+} pe_attn_args;
+
+/* ABI version of the loaded library; callers compare it with PE_ATTN_ABI_VERSION. */
+int pe_attn_abi_version(void);
+
+/* Static text for a status code. */
+const char *pe_attn_strerror(int status);
+
+/* Bytes of device workspace pe_varlen_attn_fwd needs for these arguments (host-only, from
+   n_seq, total_tokens, max_seqlen, head geometry and short_max; never reads device memory). */
+int pe_attn_workspace_size(const pe_attn_args *args, size_t *bytes);
+
+/* Packed varlen attention, both kernels in one call. Segments are routed per segment on the
+   device by their length (no host read of cu_seqlens): short ones to the LDS-resident kernel,
+   long ones through a device-built, cost-ordered tile list to the tiled MFMA kernel.
+   Replaces the reference's FlashAttention varlen leg (packed_encoders/ops.py:432-461,
+   ops.py:521-532) and the varlen candidates of select_attention
+   (packed_encoders/runtime/attention.py:66-126), GQA, causal, window and the fused sigmoid
+   gate (packed_encoders/_kernels/hybrid.py:197-219) included. */
+int pe_varlen_attn_fwd(const pe_attn_args *args, void *workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+
+/* Packed short attention: every segment through the LDS-resident short kernel. Requires
+   0 < max_seqlen <= 128 and head_dim <= 128; short_max is ignored. Needs no workspace.
+   Replaces packed_short_attention / _launch_packed_short_attention
+   (packed_encoders/_kernels/triton_packed_attention.py:175-236). */
+int pe_packed_short_attn_fwd(const pe_attn_args *args, hipStream_t stream);
+
+/* The short kernel's static launch choice for a max_seqlen (no runtime autotuning):
+   out[0] = query rows per wave (block_m), out[1] = key capacity held in LDS,
+   out[2] = heads per workgroup, out[3] = waves per workgroup.
+   Replaces select_packed_short_attention_config
+   (packed_encoders/_kernels/triton_packed_attention.py:29-42). */
+int pe_attn_short_config(int32_t max_seqlen, int32_t head_dim, int32_t out[4]);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PE_ATTN_H */

@@ -1,0 +1,58 @@
+"""Build libpe_attn.so (the HIP kernels and their C ABI) in-tree for gfx950.
+
+The library is compiled ahead of time with hipcc, next to this file, so it travels with the
+source tree; nothing is JIT-compiled at import time. ``build_library()`` always recompiles.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+INCLUDE = HERE.parent / "include"
+LIBRARY = HERE / "libpe_attn.so"
+ARCH = "gfx950"
+
+# hipcc flags. Packed FP32 instructions are disabled for device code; hipcc's host pass warns
+# that it does not know the feature, which is harmless.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+SOURCES = ["pe_attn_capi.hip"]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found: the HIP attention library cannot be built")
+    return path
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compile every HIP source into ``libpe_attn.so`` (atomic replace)."""
+    tmp = LIBRARY.with_name(f"{LIBRARY.name}.tmp{os.getpid()}")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", *(str(CSRC / s) for s in SOURCES), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "packed-fp32-ops' is not a recognized feature"
+    stderr = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        tmp.unlink(missing_ok=True)
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{' '.join(cmd)}\n{stderr}")
+    if verbose and stderr.strip():
+        print(stderr)
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))

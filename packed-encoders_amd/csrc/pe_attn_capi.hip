@@ -1,0 +1,261 @@
+// C ABI of libpe_attn.so (declared in include/pe_attn.h): argument checks, host-side sizing
+// and the launches of the plan, short and tiled kernels on the caller's stream.
+//
+// Nothing here reads device memory, synchronises or allocates, so every entry point can be
+// captured into a HIP graph. No exception crosses the ABI; failures are status codes.
+#include "../../include/pe_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+
+#include "pe_attn_device.h"
+#include "pe_attn_plan.h"
+#include "pe_attn_short.h"
+#include "pe_attn_tiled.h"
+
+namespace {
+
+using pe::AttnParams;
+
+constexpr int kDefaultShortMax = 64;  // gfx950 default routing boundary (head_dim <= 128)
+
+int gcd_int(int a, int b) {
+    while (b) {
+        const int t = a % b;
+        a = b;
+        b = t;
+    }
+    return a;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Structural checks shared by every entry point; pointers and strides only when a launch
+// will read them (workspace sizing needs sizes alone).
+int check_args(const pe_attn_args *a, bool need_pointers = true) {
+    if (!a || a->struct_size != sizeof(pe_attn_args)) return PE_ATTN_EINVAL;
+    if (a->dtype != PE_ATTN_DTYPE_BF16) return PE_ATTN_EUNSUPPORTED;
+    if (a->n_seq < 0 || a->total_tokens < 0 || a->max_seqlen < 0) return PE_ATTN_EINVAL;
+    if (a->n_heads_q < 1 || a->n_heads_kv < 1 || a->n_heads_q % a->n_heads_kv) return PE_ATTN_EINVAL;
+    if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return PE_ATTN_EUNSUPPORTED;
+    if (!(a->softmax_scale > 0.0f) || a->softmax_scale != a->softmax_scale) return PE_ATTN_EINVAL;
+    if (a->window_left < -1 || a->window_right < -1) return PE_ATTN_EINVAL;
+    if (a->causal != 0 && a->causal != 1) return PE_ATTN_EINVAL;
+    if (a->short_max < -1 || a->short_max > 128) return PE_ATTN_EINVAL;
+    if (!need_pointers || a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
+    if (!a->q || !a->k || !a->v || !a->o || !a->cu_seqlens) return PE_ATTN_EINVAL;
+    const void *ptrs[4] = {a->q, a->k, a->v, a->o};
+    for (const void *p : ptrs)
+        if (!aligned16(p)) return PE_ATTN_EINVAL;
+    const int64_t strides[8] = {a->q_stride_token, a->q_stride_head, a->k_stride_token, a->k_stride_head,
+                                a->v_stride_token, a->v_stride_head, a->o_stride_token, a->o_stride_head};
+    for (int64_t s : strides)
+        if (s < 0 || (s & 7)) return PE_ATTN_EINVAL;
+    if (a->gate) {
+        if (!aligned16(a->gate) || a->gate_stride_token < 0 || a->gate_stride_head < 0 ||
+            (a->gate_stride_token & 7) || (a->gate_stride_head & 7))
+            return PE_ATTN_EINVAL;
+    }
+    return PE_ATTN_OK;
+}
+
+int effective_short_max(const pe_attn_args *a) {
+    int s = a->short_max;
+    if (s < 0) s = a->head_dim <= 128 ? kDefaultShortMax : 0;
+    if (a->head_dim > 128) s = 0;  // the short kernel covers head_dim <= 128
+    return s;
+}
+
+int heads_per_tile(const pe_attn_args *a) { return gcd_int(a->n_heads_q / a->n_heads_kv, 4); }
+
+// Upper bound on (segment, tile) entries the plan can emit, from host-known sizes only.
+int64_t tile_capacity(const pe_attn_args *a, int short_max, int bm) {
+    if (a->n_seq == 0 || a->total_tokens == 0 || a->max_seqlen <= short_max) return 0;
+    const int64_t n = a->n_seq, t = a->total_tokens;
+    const int64_t n_long = short_max > 0 ? (t / (short_max + 1) < n ? t / (short_max + 1) : n) : n;
+    const int64_t by_shape = n * ((a->max_seqlen + bm - 1) / bm);
+    const int64_t by_tokens = (t + n_long * (bm - 1)) / bm;
+    return by_shape < by_tokens ? by_shape : by_tokens;
+}
+
+AttnParams make_params(const pe_attn_args *a, int short_max) {
+    AttnParams p;
+    std::memset(&p, 0, sizeof(p));
+    p.q = static_cast<const __bf16 *>(a->q);
+    p.k = static_cast<const __bf16 *>(a->k);
+    p.v = static_cast<const __bf16 *>(a->v);
+    p.g = static_cast<const __bf16 *>(a->gate);
+    p.o = static_cast<__bf16 *>(a->o);
+    p.cu = a->cu_seqlens;
+    p.q_st = a->q_stride_token;
+    p.q_sh = a->q_stride_head;
+    p.k_st = a->k_stride_token;
+    p.k_sh = a->k_stride_head;
+    p.v_st = a->v_stride_token;
+    p.v_sh = a->v_stride_head;
+    p.o_st = a->o_stride_token;
+    p.o_sh = a->o_stride_head;
+    p.g_st = a->gate_stride_token;
+    p.g_sh = a->gate_stride_head;
+    p.n_seq = a->n_seq;
+    p.hq = a->n_heads_q;
+    p.group = a->n_heads_q / a->n_heads_kv;
+    p.wl = a->window_left;
+    p.wr = a->window_right;
+    if (a->causal) p.wr = 0;  // causal = no key to the right of the query
+    p.short_max = short_max;
+    p.c = a->softmax_scale * pe::kLog2e;
+    return p;
+}
+
+template <int D, int SK, int HPW, bool GATE>
+int launch_short_t(const AttnParams &p, hipStream_t stream) {
+    dim3 grid(p.n_seq, (p.hq + HPW - 1) / HPW);
+    hipLaunchKernelGGL((pe::short_attn_kernel<D, SK, HPW, GATE>), grid, dim3(256), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
+}
+
+// Static short-kernel choice: key capacity SK (32/64/128) and heads per workgroup, sized so
+// the workgroup's K and V^T stay within ~75 KB of LDS (two workgroups per CU).
+void short_shape(int max_len, int d, int *sk, int *hpw) {
+    *sk = max_len <= 32 ? 32 : (max_len <= 64 ? 64 : 128);
+    if (d == 64)
+        *hpw = *sk == 128 ? 2 : 4;
+    else
+        *hpw = *sk == 32 ? 4 : (*sk == 64 ? 2 : 1);
+}
+
+template <int D, bool GATE>
+int launch_short_d(const AttnParams &p, int sk, int hpw, hipStream_t stream) {
+    if (D == 64) {
+        if (sk == 32) return launch_short_t<D, 32, 4, GATE>(p, stream);
+        if (sk == 64) return launch_short_t<D, 64, 4, GATE>(p, stream);
+        return launch_short_t<D, 128, 2, GATE>(p, stream);
+    }
+    if (sk == 32) return launch_short_t<D, 32, 4, GATE>(p, stream);
+    if (sk == 64) return launch_short_t<D, 64, 2, GATE>(p, stream);
+    return launch_short_t<D, 128, 1, GATE>(p, stream);
+    (void)hpw;
+}
+
+int launch_short(const AttnParams &p, int d, bool gate, int short_max, hipStream_t stream) {
+    int sk, hpw;
+    short_shape(short_max, d, &sk, &hpw);
+    if (d == 64) return gate ? launch_short_d<64, true>(p, sk, hpw, stream) : launch_short_d<64, false>(p, sk, hpw, stream);
+    if (d == 128) return gate ? launch_short_d<128, true>(p, sk, hpw, stream) : launch_short_d<128, false>(p, sk, hpw, stream);
+    return PE_ATTN_EUNSUPPORTED;
+}
+
+template <int D, int G, bool GATE>
+int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
+    constexpr int BN = D >= 256 ? 32 : 64;
+    p.hgroups = p.hq / G;
+    const int64_t blocks = cap * p.hgroups;
+    if (blocks <= 0) return PE_ATTN_OK;
+    if (blocks > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
+    hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, GATE>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
+}
+
+template <int D, bool GATE>
+int launch_tiled_d(const AttnParams &p, int g, int64_t cap, hipStream_t stream) {
+    if (g == 4) return launch_tiled_t<D, 4, GATE>(p, cap, stream);
+    if (g == 2) return launch_tiled_t<D, 2, GATE>(p, cap, stream);
+    return launch_tiled_t<D, 1, GATE>(p, cap, stream);
+}
+
+int launch_tiled(const AttnParams &p, int d, int g, bool gate, int64_t cap, hipStream_t stream) {
+    if (d == 64) return gate ? launch_tiled_d<64, true>(p, g, cap, stream) : launch_tiled_d<64, false>(p, g, cap, stream);
+    if (d == 128) return gate ? launch_tiled_d<128, true>(p, g, cap, stream) : launch_tiled_d<128, false>(p, g, cap, stream);
+    if (d == 256) return gate ? launch_tiled_d<256, true>(p, g, cap, stream) : launch_tiled_d<256, false>(p, g, cap, stream);
+    return PE_ATTN_EUNSUPPORTED;
+}
+
+constexpr size_t kWorkspaceHeader = 256;  // the entry count lives here, list follows aligned
+
+}  // namespace
+
+extern "C" {
+
+int pe_attn_abi_version(void) { return PE_ATTN_ABI_VERSION; }
+
+const char *pe_attn_strerror(int status) {
+    switch (status) {
+        case PE_ATTN_OK: return "ok";
+        case PE_ATTN_EINVAL: return "invalid argument";
+        case PE_ATTN_EUNSUPPORTED: return "unsupported configuration";
+        case PE_ATTN_EWORKSPACE: return "workspace missing or too small";
+        case PE_ATTN_ELAUNCH: return "kernel launch failed";
+        default: return "unknown status";
+    }
+}
+
+int pe_attn_workspace_size(const pe_attn_args *a, size_t *bytes) {
+    if (!bytes) return PE_ATTN_EINVAL;
+    const int rc = check_args(a, false);
+    if (rc) return rc;
+    const int sm = effective_short_max(a);
+    const int g = heads_per_tile(a);
+    const int64_t cap = tile_capacity(a, sm, 32 * (4 / g));
+    *bytes = cap > 0 ? kWorkspaceHeader + (size_t)cap * sizeof(int2) : 0;
+    return PE_ATTN_OK;
+}
+
+int pe_varlen_attn_fwd(const pe_attn_args *a, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    int rc = check_args(a);
+    if (rc) return rc;
+    if (a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
+    const int sm = effective_short_max(a);
+    const int g = heads_per_tile(a);
+    const int bm = 32 * (4 / g);
+    const int64_t cap = tile_capacity(a, sm, bm);
+    if (cap > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
+    if (cap > 0 && (!workspace || !aligned16(workspace) ||
+                    workspace_bytes < kWorkspaceHeader + (size_t)cap * sizeof(int2)))
+        return PE_ATTN_EWORKSPACE;
+    AttnParams p = make_params(a, sm);
+    const bool gate = a->gate != nullptr;
+    if (sm > 0) {
+        rc = launch_short(p, a->head_dim, gate, sm, stream);
+        if (rc) return rc;
+    }
+    if (cap > 0) {
+        int32_t *count = static_cast<int32_t *>(workspace);
+        int2 *work = reinterpret_cast<int2 *>(static_cast<char *>(workspace) + kWorkspaceHeader);
+        hipLaunchKernelGGL(pe::plan_kernel, dim3(1), dim3(1024), 0, stream, a->cu_seqlens, a->n_seq, sm, bm,
+                           p.wl, p.wr, work, count, (int)cap);
+        if (hipGetLastError() != hipSuccess) return PE_ATTN_ELAUNCH;
+        p.work = work;
+        p.work_count = count;
+        rc = launch_tiled(p, a->head_dim, g, gate, cap, stream);
+        if (rc) return rc;
+    }
+    return PE_ATTN_OK;
+}
+
+int pe_packed_short_attn_fwd(const pe_attn_args *a, hipStream_t stream) {
+    int rc = check_args(a, false);
+    if (rc) return rc;
+    if (a->max_seqlen <= 0 || a->max_seqlen > 128) return PE_ATTN_EUNSUPPORTED;
+    if (a->head_dim > 128) return PE_ATTN_EUNSUPPORTED;
+    rc = check_args(a);
+    if (rc) return rc;
+    if (a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
+    AttnParams p = make_params(a, a->max_seqlen);
+    return launch_short(p, a->head_dim, a->gate != nullptr, a->max_seqlen, stream);
+}
+
+int pe_attn_short_config(int32_t max_seqlen, int32_t head_dim, int32_t out[4]) {
+    if (!out || max_seqlen <= 0 || max_seqlen > 128 || (head_dim != 64 && head_dim != 128)) return PE_ATTN_EINVAL;
+    int sk, hpw;
+    short_shape(max_seqlen, head_dim, &sk, &hpw);
+    out[0] = 32;
+    out[1] = sk;
+    out[2] = hpw;
+    out[3] = 4;
+    return PE_ATTN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,141 @@
+// Device-side building blocks shared by the packed attention kernels (gfx950 / CDNA4).
+//
+// Conventions used by every kernel in this library:
+//  * A wave is 64 lanes. Lane l is split as col = l % 32, kg = l / 32.
+//  * Scores are computed transposed, S^T = K . Q^T, with v_mfma_f32_32x32x16_bf16:
+//    A = 32 keys x 16 dims (row = key col, 8 dims per lane group kg),
+//    B = 16 dims x 32 queries (query col, the same 8 dims per lane group),
+//    so after the product lane l holds, for ONE query (col) and 16 keys, the accumulator
+//    element j at key 8*(j/4) + 4*kg + (j%4) of the 32-key block. Every softmax statistic is
+//    therefore a per-lane scalar, combined with the partner lane l ^ 32 only.
+//  * The output is accumulated transposed too, O^T = V^T . P^T: A = 32 dims x 16 keys read
+//    from a transposed V tile in LDS, B = the lane's own probabilities (8 of them), so no
+//    probability ever leaves its register. Keys of every 32-key block of V^T are stored with
+//    bits 2 and 3 of the key index swapped, which makes the 8 keys lane group kg contributes
+//    to one MFMA (keys 4*kg..4*kg+3 and 8+4*kg..8+4*kg+3 of a 16-key half) contiguous.
+//    The MFMA reduces over its K dimension, so any K permutation shared by A and B is exact.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Kernel parameters (one struct for every kernel; passed by value).
+struct AttnParams {
+    const __bf16 *q, *k, *v, *g;
+    __bf16 *o;
+    const int32_t *cu;
+    int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, g_st, g_sh;
+    int32_t n_seq;
+    int32_t hq;      // query heads
+    int32_t group;   // query heads per kv head
+    int32_t wl, wr;  // window (-1: unbounded); causal already folded into wr = 0
+    int32_t short_max;
+    int32_t hgroups; // head groups per work entry (tiled kernel)
+    float c;         // softmax_scale * log2(e)
+    const int2 *work;          // tiled kernel: (segment, q-tile) entries
+    const int32_t *work_count; // tiled kernel: number of valid entries
+};
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 ld_g16(const __bf16 *p) {
+    return *reinterpret_cast<const bf16x8 *>(p);
+}
+__device__ __forceinline__ bf16x8 ld_s16(const __bf16 *p) {
+    return *reinterpret_cast<const bf16x8 *>(p);
+}
+__device__ __forceinline__ void st_s16(__bf16 *p, bf16x8 x) { *reinterpret_cast<bf16x8 *>(p) = x; }
+__device__ __forceinline__ void st_s8(__bf16 *p, bf16x4 x) { *reinterpret_cast<bf16x4 *>(p) = x; }
+
+__device__ __forceinline__ bf16x8 zero8() {
+    bf16x8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (__bf16)0.0f;
+    return z;
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Position of key k inside a 32-key block of the transposed V tile (bits 2 and 3 swapped).
+__device__ __forceinline__ int vperm(int k) {
+    return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+// Key index (within its 32-key block) of accumulator element j held by lane group kg.
+__device__ __forceinline__ int acc_key(int j, int kg) { return 8 * (j >> 2) + 4 * kg + (j & 3); }
+
+// Round 8 fp32 probabilities to bf16 (round to nearest even) as one MFMA operand.
+__device__ __forceinline__ bf16x8 to_bf16x8(const f32x16 &s, int base) {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = (__bf16)s[base + i];
+    return r;
+}
+
+// Transpose four 8-dim key rows (a 4-key x 8-dim chunk) into eight 4-key dim rows of V^T.
+// vt points at the chunk's first dim row, already offset to the permuted key position;
+// pitch is the V^T row pitch in elements.
+__device__ __forceinline__ void store_vt_chunk(__bf16 *vt, int pitch, const bf16x8 (&rows)[4]) {
+#pragma unroll
+    for (int dd = 0; dd < 8; ++dd) {
+        bf16x4 t;
+        t[0] = rows[0][dd];
+        t[1] = rows[1][dd];
+        t[2] = rows[2][dd];
+        t[3] = rows[3][dd];
+        st_s8(vt + dd * pitch, t);
+    }
+}
+
+// Whether key block [kb0, kb0 + 32) intersects the keys any row in [r0, r1) may read.
+__device__ __forceinline__ bool block_live(int kb0, int L, int r0, int r1, int wl, int wr) {
+    if (kb0 >= L) return false;
+    if (wl >= 0 && kb0 + 31 < r0 - wl) return false;
+    if (wr >= 0 && kb0 > r1 - 1 + wr) return false;
+    return true;
+}
+
+// Whether every (row, key) of rows [r0, r1) x keys [kb0, kb0 + 32) is allowed (no masking).
+__device__ __forceinline__ bool block_full(int kb0, int L, int r0, int r1, int wl, int wr) {
+    if (kb0 + 32 > L) return false;
+    if (wl >= 0 && (r1 - 1) - kb0 > wl) return false;
+    if (wr >= 0 && (kb0 + 31) - r0 > wr) return false;
+    return true;
+}
+
+// Store 4 consecutive output dims of one row, with the optional fused sigmoid gate:
+// y = bf16(bf16(o) * bf16(sigmoid(g))) (the rounding order of the reference's gate kernel,
+// packed_encoders/_kernels/hybrid.py:197-206).
+template <bool GATE>
+__device__ __forceinline__ void store_out4(__bf16 *orow, const __bf16 *grow, float a0, float a1,
+                                           float a2, float a3) {
+    bf16x4 r;
+    r[0] = (__bf16)a0;
+    r[1] = (__bf16)a1;
+    r[2] = (__bf16)a2;
+    r[3] = (__bf16)a3;
+    if constexpr (GATE) {
+        bf16x4 g = *reinterpret_cast<const bf16x4 *>(grow);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float gs = 1.0f / (1.0f + __expf(-(float)g[i]));
+            float sg = (float)(__bf16)gs;
+            r[i] = (__bf16)((float)r[i] * sg);
+        }
+    }
+    *reinterpret_cast<bf16x4 *>(orow) = r;
+}
+
+}  // namespace pe

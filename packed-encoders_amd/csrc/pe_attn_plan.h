@@ -1,0 +1,71 @@
+// Device-side work planning for the tiled kernel: no host read of cu_seqlens, capture-safe.
+//
+// One 1024-thread workgroup reads cu_seqlens, keeps the segments longer than short_max, splits
+// each into BM-row query tiles and writes (segment, tile) entries ordered by decreasing cost
+// (keys a tile visits: the whole segment, its band, or its causal prefix). Costs are bucketed
+// at half-octave resolution, a counting sort in LDS, so the tiled grid dispatches the
+// longest-running tiles first (longest-processing-time order) and the tail is made of short
+// tiles. Consecutive tiles of a segment with equal cost stay adjacent, so a segment's K/V is
+// read by neighbouring workgroups. Order within a bucket depends on atomics; it changes only
+// the schedule, never a result: every output row is produced by exactly one workgroup.
+#pragma once
+
+#include "pe_attn_device.h"
+
+namespace pe {
+
+__device__ __forceinline__ int plan_tile_cost(int t, int bm, int L, int wl, int wr) {
+    const int r0 = t * bm, r1 = min(L, r0 + bm);
+    const int klo = wl >= 0 ? max(0, r0 - wl) : 0;
+    const int khi = wr >= 0 ? min(L, r1 + wr) : L;
+    return max(1, khi - klo);
+}
+
+__device__ __forceinline__ int plan_bucket(int cost) {
+    const int lg = 31 - __clz(cost);
+    const int half = lg >= 1 ? (cost >> (lg - 1)) & 1 : 0;
+    return min(63, 2 * lg + half);
+}
+
+__global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, int n_seq, int short_max, int bm,
+                                                    int wl, int wr, int2 *work, int32_t *count, int cap) {
+    __shared__ int cnt[64];
+    __shared__ int off[64];
+    const int tid = threadIdx.x;
+    if (tid < 64) cnt[tid] = 0;
+    __syncthreads();
+    for (int seg = tid; seg < n_seq; seg += blockDim.x) {
+        const int L = cu[seg + 1] - cu[seg];
+        if (L <= short_max) continue;
+        const int nt = (L + bm - 1) / bm;
+        for (int t = 0; t < nt; ++t) atomicAdd(&cnt[plan_bucket(plan_tile_cost(t, bm, L, wl, wr))], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int b = 63; b >= 0; --b) {
+            off[b] = run;
+            run += cnt[b];
+        }
+        *count = min(run, cap);
+    }
+    __syncthreads();
+    for (int seg = tid; seg < n_seq; seg += blockDim.x) {
+        const int L = cu[seg + 1] - cu[seg];
+        if (L <= short_max) continue;
+        const int nt = (L + bm - 1) / bm;
+        int t = 0;
+        while (t < nt) {
+            // A run of consecutive tiles in one cost bucket gets one contiguous reservation.
+            const int b = plan_bucket(plan_tile_cost(t, bm, L, wl, wr));
+            int e = t + 1;
+            while (e < nt && plan_bucket(plan_tile_cost(e, bm, L, wl, wr)) == b) ++e;
+            const int pos = atomicAdd(&off[b], e - t);
+            for (int i = 0; i < e - t; ++i)
+                if (pos + i < cap) work[pos + i] = make_int2(seg, t + i);
+            t = e;
+        }
+    }
+}
+
+}  // namespace pe

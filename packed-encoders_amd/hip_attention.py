@@ -1,0 +1,240 @@
+"""HIP packed varlen attention for MI355X (gfx950), registered as torch ops.
+
+The operator surface of the reference's packed attention kernel module
+(packed_encoders/_kernels/triton_packed_attention.py): ``packed_short_attention``,
+``packed_short_attention_supported`` and ``select_packed_short_attention_config`` keep their
+names, argument meaning and error behaviour (``ValueError`` outside the envelope), and
+``varlen_attention`` is the general form (long segments, GQA, causal, windows, fused sigmoid
+gate) that replaces the reference's FlashAttention varlen calls.
+
+All compute goes through ``libpe_attn.so`` (include/pe_attn.h) on the current HIP stream via
+the ``pe_hip::varlen_attention`` / ``pe_hip::packed_short_attention`` torch ops. There is no
+CPU or eager-PyTorch fallback: if the library is missing, the loader raises ``ImportError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_BF16 = torch.bfloat16
+
+
+def _row_aligned(t: Tensor) -> bool:
+    # 16-byte rows: base pointer and token/head strides (elements) on 8-element boundaries.
+    return t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0
+
+
+def _aligned(t: Tensor) -> Tensor:
+    return t if _row_aligned(t) else t.contiguous()
+
+
+def _args(q: Tensor, k: Tensor, v: Tensor, o: Tensor, cu: Tensor, max_seqlen: int, scale: float,
+          window_left: int, window_right: int, causal: bool, gate: Tensor | None,
+          short_max: int) -> _lib.AttnArgs:
+    a = _lib.AttnArgs()
+    a.struct_size = ctypes.sizeof(_lib.AttnArgs)
+    a.dtype = _lib.DTYPE_BF16
+    a.q, a.k, a.v, a.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    a.gate = gate.data_ptr() if gate is not None else None
+    a.cu_seqlens = cu.data_ptr()
+    a.q_stride_token, a.q_stride_head = q.stride(0), q.stride(1)
+    a.k_stride_token, a.k_stride_head = k.stride(0), k.stride(1)
+    a.v_stride_token, a.v_stride_head = v.stride(0), v.stride(1)
+    a.o_stride_token, a.o_stride_head = o.stride(0), o.stride(1)
+    if gate is not None:
+        a.gate_stride_token, a.gate_stride_head = gate.stride(0), gate.stride(1)
+    a.n_seq = cu.numel() - 1
+    a.total_tokens = q.shape[0]
+    a.max_seqlen = int(max_seqlen)
+    a.n_heads_q, a.n_heads_kv, a.head_dim = q.shape[1], k.shape[1], q.shape[2]
+    a.softmax_scale = float(scale)
+    a.window_left, a.window_right = int(window_left), int(window_right)
+    a.causal = 1 if causal else 0
+    a.short_max = int(short_max)
+    return a
+
+
+def _check_tensors(q: Tensor, k: Tensor, v: Tensor, cu: Tensor, gate: Tensor | None) -> None:
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+        raise ValueError("varlen attention expects [tokens, heads, head_dim] q/k/v")
+    if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
+    if q.shape[1] % k.shape[1]:
+        raise ValueError("query heads must be a multiple of kv heads")
+    if q.dtype != _BF16 or k.dtype != _BF16 or v.dtype != _BF16:
+        raise ValueError("varlen attention computes in bf16")
+    if cu.dtype != torch.int32 or cu.ndim != 1 or cu.numel() < 1:
+        raise ValueError("cu_seqlens must be a 1-D int32 tensor [n_seq + 1]")
+    devices = {q.device, k.device, v.device, cu.device}
+    if gate is not None:
+        if gate.shape != q.shape or gate.dtype != _BF16:
+            raise ValueError("gate must be bf16 with q's shape")
+        devices.add(gate.device)
+    if len(devices) != 1 or q.device.type != "cuda":
+        raise ValueError("q, k, v, cu_seqlens (and gate) must be on one HIP device")
+
+
+def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int,
+                 softmax_scale: float, window_left: int, window_right: int, causal: bool,
+                 gate: Tensor | None, short_max: int) -> Tensor:
+    _check_tensors(q, k, v, cu_seqlens, gate)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    gate = _aligned(gate) if gate is not None else None
+    out = torch.empty(q.shape, dtype=_BF16, device=q.device)
+    if q.shape[0] == 0 or cu_seqlens.numel() < 2:
+        return out
+    lib = _lib.library()
+    args = _args(q, k, v, out, cu_seqlens, max_seqlen, softmax_scale, window_left, window_right,
+                 causal, gate, short_max)
+    size = ctypes.c_size_t(0)
+    _lib.check(lib.pe_attn_workspace_size(ctypes.byref(args), ctypes.byref(size)), "pe_attn_workspace_size")
+    workspace = torch.empty(size.value, dtype=torch.uint8, device=q.device) if size.value else None
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    status = lib.pe_varlen_attn_fwd(ctypes.byref(args), workspace.data_ptr() if workspace is not None else None,
+                                    size.value, stream)
+    _lib.check(status, "pe_varlen_attn_fwd")
+    return out
+
+
+def _short_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int,
+                softmax_scale: float, window_left: int, window_right: int) -> Tensor:
+    _check_tensors(q, k, v, cu_seqlens, None)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    out = torch.empty(q.shape, dtype=_BF16, device=q.device)
+    if q.shape[0] == 0 or cu_seqlens.numel() < 2:
+        return out
+    lib = _lib.library()
+    args = _args(q, k, v, out, cu_seqlens, max_seqlen, softmax_scale, window_left, window_right,
+                 False, None, 0)
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    _lib.check(lib.pe_packed_short_attn_fwd(ctypes.byref(args), stream), "pe_packed_short_attn_fwd")
+    return out
+
+
+def _meta(q: Tensor, *args, **kwargs) -> Tensor:
+    return torch.empty(q.shape, dtype=_BF16, device=q.device)
+
+
+def _register() -> None:
+    """Define ``pe_hip::varlen_attention`` and ``pe_hip::packed_short_attention`` once per process."""
+    lib = torch.library.Library("pe_hip", "FRAGMENT")
+    try:
+        lib.define("varlen_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, int max_seqlen, "
+                   "float softmax_scale, int window_left, int window_right, bool causal, Tensor? gate, "
+                   "int short_max) -> Tensor")
+        lib.define("packed_short_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, int max_seqlen, "
+                   "float softmax_scale, int window_left, int window_right) -> Tensor")
+    except RuntimeError:
+        return  # already defined by an earlier import in this process
+    lib.impl("varlen_attention", _varlen_impl, "CUDA")
+    lib.impl("varlen_attention", _meta, "Meta")
+    lib.impl("packed_short_attention", _short_impl, "CUDA")
+    lib.impl("packed_short_attention", _meta, "Meta")
+    globals()["_TORCH_LIBRARY"] = lib
+
+
+_register()
+
+
+def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int, *,
+                     softmax_scale: float | None = None, window: tuple[int, int] = (-1, -1),
+                     causal: bool = False, gate: Tensor | None = None,
+                     short_max: int | None = None) -> Tensor:
+    """Packed varlen attention: q ``[T, Hq, D]``, k/v ``[T, Hkv, D]`` bf16, int32 ``cu_seqlens``.
+
+    ``window=(left, right)`` bounds ``i - j <= left`` and ``j - i <= right`` (-1 unbounded,
+    the FlashAttention convention of packed_encoders/ops.py:404-461); ``causal`` forbids
+    ``j > i``; ``gate`` multiplies the output by ``bf16(sigmoid(gate))``. ``short_max`` routes
+    segments of at most that length to the LDS-resident short kernel (None: the gfx950 policy
+    default). Returns a new contiguous ``[T, Hq, D]``; rows beyond ``cu_seqlens[-1]`` are not
+    written. Forward only.
+    """
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        raise ValueError("the HIP packed attention is forward-only; call it under torch.no_grad()")
+    scale = q.shape[-1] ** -0.5 if softmax_scale is None else float(softmax_scale)
+    if short_max is None:
+        short_max = -1
+    return torch.ops.pe_hip.varlen_attention(q, k, v, cu_seqlens, int(max_seqlen), scale,
+                                             int(window[0]), int(window[1]), bool(causal), gate,
+                                             int(short_max))
+
+
+def packed_short_attention_supported(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor,
+                                     max_seqlen: int, *, half_window: int | None) -> bool:
+    """Pure capability predicate (host metadata only; the reference's
+    triton_packed_attention.py:146-172). Wider than the reference's envelope: any head count,
+    head_dim 64 or 128 and any non-negative half window; still bf16, Smax <= 128, no grad."""
+    return (
+        q.is_cuda and k.is_cuda and v.is_cuda and cu_seqlens.is_cuda
+        and q.ndim == k.ndim == v.ndim == 3
+        and q.shape == k.shape == v.shape
+        and q.shape[2] in (64, 128)
+        and q.dtype == k.dtype == v.dtype == _BF16
+        and q.stride(-1) == k.stride(-1) == v.stride(-1) == 1
+        and cu_seqlens.dtype == torch.int32
+        and cu_seqlens.ndim == 1
+        and cu_seqlens.numel() >= 2
+        and 0 < int(max_seqlen) <= 128
+        and (half_window is None or int(half_window) >= 0)
+        and not torch.is_grad_enabled()
+    )
+
+
+def packed_short_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int, *,
+                           half_window: int | None, softmax_scale: float) -> Tensor:
+    """Packed non-causal self attention over short segments; returns contiguous ``[M, H, D]``.
+
+    Same contract as the reference's ``packed_short_attention``
+    (triton_packed_attention.py:175-196): ``half_window`` None is global attention within each
+    segment, an int ``w`` the symmetric band ``|i - j| <= w``; ``ValueError`` outside the
+    envelope."""
+    if not packed_short_attention_supported(q, k, v, cu_seqlens, max_seqlen, half_window=half_window):
+        raise ValueError(
+            "packed short attention requires no-grad HIP bf16 [M,H,64|128] Q/K/V, int32 "
+            "cu_seqlens, Smax<=128, and global or non-negative half-window attention"
+        )
+    w = -1 if half_window is None else int(half_window)
+    return torch.ops.pe_hip.packed_short_attention(q, k, v, cu_seqlens, int(max_seqlen),
+                                                   float(softmax_scale), w, w)
+
+
+def select_packed_short_attention_config(max_seqlen: int, head_dim: int = 64) -> dict[str, int]:
+    """The short kernel's static launch choice for ``max_seqlen`` in JSON-friendly form (the
+    reference's triton_packed_attention.py:40-42; the fields describe this kernel's tiles)."""
+    out = (ctypes.c_int32 * 4)()
+    _lib.check(_lib.library().pe_attn_short_config(int(max_seqlen), int(head_dim), out),
+               "pe_attn_short_config")
+    return {"block_m": out[0], "key_capacity": out[1], "heads_per_workgroup": out[2], "num_waves": out[3]}
+
+
+def useful_flops(lengths, n_heads_q: int, head_dim: int, *, window: tuple[int, int] = (-1, -1),
+                 causal: bool = False) -> int:
+    """``4 * D * Hq * sum(allowed (query, key) pairs)`` over live tokens only."""
+    return 4 * head_dim * n_heads_q * sum(allowed_pairs(int(n), window, causal) for n in lengths)
+
+
+def allowed_pairs(n: int, window: tuple[int, int] = (-1, -1), causal: bool = False) -> int:
+    """Number of (i, j) in [0, n)^2 with ``i - j <= left`` and ``j - i <= right`` (causal: right 0)."""
+    left, right = window
+    right = 0 if causal else right
+    left = n if left < 0 else min(left, n)
+    right = n if right < 0 else min(right, n)
+    # pairs with j <= i and i - j <= left, plus pairs with j > i and j - i <= right
+    below = sum(n - d for d in range(0, left + 1) if d < n)
+    above = sum(n - d for d in range(1, right + 1) if d < n)
+    return below + above
+
+
+__all__ = [
+    "packed_short_attention",
+    "packed_short_attention_supported",
+    "select_packed_short_attention_config",
+    "varlen_attention",
+    "useful_flops",
+    "allowed_pairs",
+]

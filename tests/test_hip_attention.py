@@ -1,0 +1,243 @@
+"""GPU parity of the HIP packed attention kernels against the CPU oracle (oracle/attention.py).
+
+Bar (the reference's tolerances): max-abs <= 2e-2 (runtime/attention.py:40), per-token cosine
+>= 0.9999, mean-abs close to what bf16 inputs and outputs allow, and bit-exact invariants:
+zero cross-segment leakage, determinism, independence from batch composition
+(tests/test_packed_short_attention.py:97-147 and tests/test_cpu_short_attention.py:72-77).
+Inputs are drawn in fp32 on the CPU, rounded to bf16 for the GPU; the oracle reads the same
+bf16 values in float64.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MIN_COS = 0.9999
+
+
+def _inputs(lengths, hq=12, hkv=None, d=64, seed=0, logit_scale=1.0, gate=False):
+    hkv = hq if hkv is None else hkv
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lengths)
+    q = (torch.randn(T, hq, d, generator=g) * logit_scale).bfloat16()
+    k = (torch.randn(T, hkv, d, generator=g) * logit_scale).bfloat16()
+    v = torch.randn(T, hkv, d, generator=g).bfloat16()
+    gt = torch.randn(T, hq, d, generator=g).bfloat16() if gate else None
+    cu = torch.tensor([0, *np.cumsum(lengths).tolist()], dtype=torch.int32)
+    return q, k, v, cu, gt
+
+
+def _dev(*ts):
+    return [None if t is None else t.cuda() for t in ts]
+
+
+def _oracle(q, k, v, cu, *, scale, window=(-1, -1), causal=False, gate=None):
+    f = lambda t: t.float().numpy()
+    return oa.packed_attention(f(q), f(k), f(v), cu.numpy(), scale=scale, window=window, causal=causal,
+                               gate=None if gate is None else f(gate))
+
+
+def _assert_parity(got, want, cu, *, max_abs=MAX_ABS, min_cos=MIN_COS):
+    got = got.float().cpu().numpy().astype(np.float64)
+    live = np.zeros(got.shape[0], dtype=bool)
+    c = cu.tolist()
+    for a, b in zip(c, c[1:]):
+        live[a:b] = True
+    g, w = got[live], want[live]
+    assert np.isfinite(g).all()
+    err = np.abs(g - w)
+    assert err.max() <= max_abs, f"max abs {err.max():.4g}"
+    cos = oa.cosine_per_token(g, w)
+    assert cos.min() >= min_cos, f"min cosine {cos.min():.6f}"
+    return float(err.max()), float(err.mean())
+
+
+SHORT_LENGTHS = [
+    [1, 2, 31, 32, 33, 63, 64, 65, 127, 128],
+    [128] * 8,
+    [128, 64, 16, 16, 16, 16, 16, 16],
+    [46, 46, 45, 45, 45, 44, 43, 42],
+]
+
+
+@pytest.mark.parametrize("half_window", [None, 64])
+@pytest.mark.parametrize("lengths", SHORT_LENGTHS, ids=["ragged", "128x8", "mixed", "agentir"])
+def test_packed_short_attention_matches_oracle(pe, lengths, half_window):
+    announce(f"packed_short lengths={lengths[:4]} half={half_window}")
+    q, k, v, cu, _ = _inputs(lengths, seed=17)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    with torch.inference_mode():
+        got = pe.packed_short_attention(qd, kd, vd, cud, max(lengths), half_window=half_window,
+                                        softmax_scale=0.125)
+    window = (-1, -1) if half_window is None else (half_window, half_window)
+    want = _oracle(q, k, v, cu, scale=0.125, window=window)
+    _, mean = _assert_parity(got, want, cu)
+    # bf16 output rounding alone gives ~1e-3 mean error on these magnitudes
+    assert mean < 4e-3
+
+
+LONG_CASES = [
+    ([1, 300, 1000, 129, 2048, 64, 7], (-1, -1), False),
+    ([1, 300, 1000, 129, 2048, 64, 7], (64, 64), False),
+    ([1, 300, 1000, 129, 513, 64, 7], (-1, -1), True),
+    ([700, 33, 0, 250], (10, 3), False),
+    ([4096], (-1, -1), False),
+]
+
+
+@pytest.mark.parametrize("short_max", [0, 64, 128])
+@pytest.mark.parametrize("lengths,window,causal", LONG_CASES, ids=["global", "band64", "causal", "asym", "4k"])
+def test_varlen_attention_matches_oracle(pe, lengths, window, causal, short_max):
+    announce(f"varlen lengths={lengths} window={window} causal={causal} short_max={short_max}")
+    q, k, v, cu, _ = _inputs(lengths, hq=4, seed=3)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    with torch.inference_mode():
+        got = pe.varlen_attention(qd, kd, vd, cud, max(lengths), softmax_scale=0.125, window=window,
+                                  causal=causal, short_max=short_max)
+    want = _oracle(q, k, v, cu, scale=0.125, window=window, causal=causal)
+    _assert_parity(got, want, cu)
+
+
+@pytest.mark.parametrize("d,hq,hkv", [(64, 8, 2), (128, 6, 3), (128, 4, 4), (256, 8, 2), (256, 8, 1), (64, 16, 2)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa_head_dims(pe, d, hq, hkv, causal):
+    lengths = [16, 200, 5, 77, 512]
+    announce(f"gqa d={d} hq={hq} hkv={hkv} causal={causal}")
+    q, k, v, cu, _ = _inputs(lengths, hq=hq, hkv=hkv, d=d, seed=11)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    with torch.inference_mode():
+        got = pe.varlen_attention(qd, kd, vd, cud, max(lengths), causal=causal)
+    want = _oracle(q, k, v, cu, scale=d ** -0.5, causal=causal)
+    _assert_parity(got, want, cu)
+
+
+@pytest.mark.parametrize("d,short_max", [(256, 0), (64, 64), (128, 32)])
+def test_fused_sigmoid_gate(pe, d, short_max):
+    lengths = [16, 300, 40, 129]
+    announce(f"gate d={d}")
+    q, k, v, cu, g = _inputs(lengths, hq=8, hkv=2, d=d, seed=13, gate=True)
+    qd, kd, vd, cud, gd = _dev(q, k, v, cu, g)
+    with torch.inference_mode():
+        got = pe.varlen_attention(qd, kd, vd, cud, max(lengths), causal=True, gate=gd, short_max=short_max)
+    want = _oracle(q, k, v, cu, scale=d ** -0.5, causal=True, gate=g)
+    _assert_parity(got, want, cu)
+
+
+@pytest.mark.parametrize("logit_scale", [0.01, 1.0, 8.0])
+@pytest.mark.parametrize("short_max", [0, 128])
+def test_softmax_stability_and_determinism(pe, logit_scale, short_max):
+    lengths = [33, 65, 127]
+    announce(f"stability scale={logit_scale} short_max={short_max}")
+    q, k, v, cu, _ = _inputs(lengths, seed=11, logit_scale=logit_scale)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    with torch.inference_mode():
+        first = pe.varlen_attention(qd, kd, vd, cud, 127, softmax_scale=0.125, window=(64, 64), short_max=short_max)
+        second = pe.varlen_attention(qd, kd, vd, cud, 127, softmax_scale=0.125, window=(64, 64), short_max=short_max)
+    assert torch.isfinite(first).all()
+    assert torch.equal(first, second)
+
+
+@pytest.mark.parametrize("short_max", [0, 128])
+def test_no_cross_sequence_leakage(pe, short_max):
+    lengths = [31, 65, 300]
+    announce(f"leakage short_max={short_max}")
+    q, k, v, cu, _ = _inputs(lengths, seed=7)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    with torch.inference_mode():
+        base = pe.varlen_attention(qd, kd, vd, cud, 300, softmax_scale=0.125, short_max=short_max)
+        k2, v2 = kd.clone(), vd.clone()
+        k2[31:96] *= 100
+        v2[31:96] *= -100
+        changed = pe.varlen_attention(qd, k2, v2, cud, 300, softmax_scale=0.125, short_max=short_max)
+    assert torch.equal(base[:31], changed[:31])
+    assert torch.equal(base[96:], changed[96:])
+
+
+def test_segment_alone_equals_segment_in_batch(pe):
+    lengths = [50, 700, 20]
+    announce("batch independence")
+    q, k, v, cu, _ = _inputs(lengths, seed=9)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    with torch.inference_mode():
+        batch = pe.varlen_attention(qd, kd, vd, cud, 700, window=(64, 64))
+        for a, b in ((0, 50), (50, 750), (750, 770)):
+            one = torch.tensor([0, b - a], dtype=torch.int32, device="cuda")
+            alone = pe.varlen_attention(qd[a:b].contiguous(), kd[a:b].contiguous(), vd[a:b].contiguous(), one, b - a,
+                                        window=(64, 64))
+            assert torch.equal(alone, batch[a:b])
+
+
+def test_strided_v_view_of_packed_qkv(pe):
+    # v as the reference passes it: a view into qkv [T, 3*H*D] (token stride 3*H*D)
+    lengths = [40, 200]
+    T, h, d = sum(lengths), 12, 64
+    announce("strided v")
+    g = torch.Generator().manual_seed(21)
+    qkv = torch.randn(T, 3 * h * d, generator=g).bfloat16()
+    cu = torch.tensor([0, 40, 240], dtype=torch.int32)
+    q = qkv.view(T, 3, h, d)[:, 0].contiguous()
+    k = qkv.view(T, 3, h, d)[:, 1].contiguous()
+    qkvd = qkv.cuda()
+    v_view = qkvd.view(T, 3, h, d)[:, 2]
+    assert v_view.stride(0) == 3 * h * d
+    with torch.inference_mode():
+        got = pe.varlen_attention(q.cuda(), k.cuda(), v_view, cu.cuda(), 200, softmax_scale=0.125)
+    want = _oracle(q, k, qkv.view(T, 3, h, d)[:, 2], cu, scale=0.125)
+    _assert_parity(got, want, cu)
+
+
+def test_rows_beyond_last_boundary_and_empty_segments_untouched(pe):
+    from packed_encoders_amd import _lib
+    from packed_encoders_amd.hip_attention import _args
+
+    lengths = [0, 20, 0, 130, 0]
+    T = sum(lengths) + 24  # 24 padding rows beyond cu[-1]
+    announce("untouched rows")
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(T, 4, 64, generator=g).bfloat16().cuda() for _ in range(3))
+    cu = torch.tensor([0, *np.cumsum(lengths).tolist()], dtype=torch.int32, device="cuda")
+    out = torch.full((T, 4, 64), 7.0, dtype=torch.bfloat16, device="cuda")
+    lib = _lib.library()
+    for short_max in (0, 64):
+        a = _args(q, k, v, out, cu, 130, 0.125, -1, -1, False, None, short_max)
+        size = ctypes.c_size_t()
+        assert lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size)) == 0
+        ws = torch.empty(max(size.value, 1), dtype=torch.uint8, device="cuda")
+        rc = lib.pe_varlen_attn_fwd(ctypes.byref(a), ws.data_ptr(), size.value, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert torch.all(out[150:] == 7.0)
+        want = _oracle(q.cpu(), k.cpu(), v.cpu(), cu.cpu(), scale=0.125)
+        _assert_parity(out, want, cu.cpu())
+
+
+def test_workspace_too_small_is_reported(pe):
+    from packed_encoders_amd import _lib
+    from packed_encoders_amd.hip_attention import _args
+
+    q = torch.zeros(300, 2, 64, dtype=torch.bfloat16, device="cuda")
+    cu = torch.tensor([0, 300], dtype=torch.int32, device="cuda")
+    a = _args(q, q, q, q.clone(), cu, 300, 0.125, -1, -1, False, None, 0)
+    ws = torch.empty(16, dtype=torch.uint8, device="cuda")
+    assert _lib.library().pe_varlen_attn_fwd(ctypes.byref(a), ws.data_ptr(), 16, None) == -3
+
+
+def test_out_of_envelope_raises_value_error(pe):
+    q, k, v, cu, _ = _dev(*_inputs([32, 17], seed=1))
+    with torch.inference_mode():
+        assert pe.packed_short_attention_supported(q, k, v, cu, 32, half_window=None)
+        assert not pe.packed_short_attention_supported(q, k, v, cu, 129, half_window=None)
+        with pytest.raises(ValueError):
+            pe.packed_short_attention(q, k, v, cu, 129, half_window=None, softmax_scale=0.125)
+        with pytest.raises(ValueError):
+            pe.varlen_attention(q.float(), k, v, cu, 32)

@@ -1,0 +1,137 @@
+"""libpe_attn.so loads on the CPU host and exports every entry point include/pe_attn.h declares.
+
+Only host-side entry points are called here (ABI version, status text, workspace sizing, the
+static short-kernel table and argument rejection); nothing launches a kernel.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "pe_attn.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s+\**\s*(pe_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib(pe):
+    from packed_encoders_amd import _lib
+
+    return _lib.library()
+
+
+def test_header_declares_the_expected_entry_points():
+    from packed_encoders_amd import _lib
+
+    assert _declared() == sorted(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from packed_encoders_amd import _build
+
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_build.LIBRARY)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    for name in _declared():
+        assert name in exported, name
+        assert hasattr(lib, name)
+
+
+def test_library_holds_gfx950_code():
+    from packed_encoders_amd import _build
+
+    data = _build.LIBRARY.read_bytes()
+    assert b"gfx950" in data
+
+
+def test_abi_version_and_status_text(lib):
+    assert lib.pe_attn_abi_version() == 1
+    assert lib.pe_attn_strerror(0) == b"ok"
+    assert lib.pe_attn_strerror(-3) == b"workspace missing or too small"
+    assert lib.pe_attn_strerror(-99) == b"unknown status"
+
+
+def _args(**kw):
+    from packed_encoders_amd import _lib
+
+    a = _lib.AttnArgs()
+    a.struct_size = ctypes.sizeof(_lib.AttnArgs)
+    a.dtype = 1
+    a.n_seq, a.total_tokens, a.max_seqlen = 64, 32438, 2048
+    a.n_heads_q, a.n_heads_kv, a.head_dim = 12, 12, 64
+    a.softmax_scale = 0.125
+    a.window_left = a.window_right = -1
+    a.short_max = -1
+    for name, value in kw.items():
+        setattr(a, name, value)
+    return a
+
+
+def _ws(lib, a):
+    size = ctypes.c_size_t(12345)
+    rc = lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size))
+    return rc, size.value
+
+
+def test_workspace_size_is_host_arithmetic(lib):
+    # 64 segments, max 2048: tiles of 128 rows; bound min(N*ceil(S/128), (T + N_long*127)/128)
+    rc, size = _ws(lib, _args())
+    assert rc == 0
+    n_long = min(64, 32438 // 65)
+    cap = min(64 * 16, (32438 + n_long * 127) // 128)
+    assert size == 256 + 8 * cap
+    # every segment fits the short kernel: no workspace
+    rc, size = _ws(lib, _args(max_seqlen=64))
+    assert rc == 0 and size == 0
+    # GQA 4:1 packs 4 heads per tile: 32-row tiles
+    rc, size = _ws(lib, _args(n_heads_q=8, n_heads_kv=2, head_dim=256, max_seqlen=512, n_seq=256, total_tokens=71104))
+    assert rc == 0
+    assert size == 256 + 8 * min(256 * 16, (71104 + 256 * 31) // 32)
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("struct_size", 8, -1), ("dtype", 7, -2), ("head_dim", 96, -2), ("n_heads_kv", 5, -1),
+    ("softmax_scale", 0.0, -1), ("window_left", -2, -1), ("causal", 2, -1), ("short_max", 129, -1),
+])
+def test_bad_arguments_are_rejected_before_any_launch(lib, field, value, status):
+    rc, _ = _ws(lib, _args(**{field: value}))
+    assert rc == status
+    a = _args(**{field: value})
+    assert lib.pe_varlen_attn_fwd(ctypes.byref(a), None, 0, None) == status
+
+
+def test_missing_device_pointers_are_rejected(lib):
+    a = _args()  # q/k/v/o/cu are NULL with work to do
+    assert lib.pe_varlen_attn_fwd(ctypes.byref(a), None, 0, None) == -1
+    assert lib.pe_packed_short_attn_fwd(ctypes.byref(_args(max_seqlen=64)), None) == -1
+    assert lib.pe_packed_short_attn_fwd(ctypes.byref(_args(max_seqlen=129)), None) == -2
+
+
+def test_empty_batch_is_a_no_op(lib):
+    a = _args(n_seq=0, total_tokens=0)
+    assert lib.pe_varlen_attn_fwd(ctypes.byref(a), None, 0, None) == 0
+
+
+def test_short_config_table(lib):
+    out = (ctypes.c_int32 * 4)()
+    expected = {1: (32, 32, 4, 4), 32: (32, 32, 4, 4), 33: (32, 64, 4, 4), 64: (32, 64, 4, 4),
+                65: (32, 128, 2, 4), 128: (32, 128, 2, 4)}
+    for max_seqlen, want in expected.items():
+        assert lib.pe_attn_short_config(max_seqlen, 64, out) == 0
+        assert tuple(out) == want
+    assert lib.pe_attn_short_config(129, 64, out) == -1
+    assert lib.pe_attn_short_config(64, 256, out) == -1
+
+
+def test_python_config_mirror(pe):
+    cfg = pe.select_packed_short_attention_config(100)
+    assert cfg == {"block_m": 32, "key_capacity": 128, "heads_per_workgroup": 2, "num_waves": 4}

@@ -1,0 +1,161 @@
+"""Pins the CPU oracle (oracle/attention.py) before any GPU result is compared with it.
+
+Each check is chosen so that a plausible mistake in the oracle fails it: a dropped scale, a
+transposed operand, an off-by-one band edge, a wrong GQA head mapping or a wrong bf16 rounding.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+
+
+def _rand(rng, *shape):
+    return rng.standard_normal(shape).astype(np.float32)
+
+
+def _cu(lengths):
+    return np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+
+
+def test_to_bf16_matches_torch_rounding():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10.0,
+        # exact ties between two bf16 neighbours (low 16 bits = 0x8000), both parities
+        (np.arange(1, 2000, dtype=np.uint32) << 16 | 0x8000).view(np.float32),
+        np.array([0.0, -0.0, 1e-40, -1e-40, 3.3895e38, np.inf, -np.inf], dtype=np.float32),
+    ])
+    ours = oa.to_bf16(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+    assert np.isnan(oa.to_bf16(np.array([np.nan], dtype=np.float32))).all()
+
+
+@pytest.mark.parametrize("window,causal", [((-1, -1), False), ((2, 2), False), ((0, 3), False),
+                                           ((-1, -1), True), ((1, -1), False)])
+def test_vectorised_oracle_matches_brute_force(window, causal):
+    rng = np.random.default_rng(1)
+    lengths = [1, 5, 0, 7, 3]
+    T = sum(lengths)
+    q, k, v = _rand(rng, T, 4, 8), _rand(rng, T, 2, 8), _rand(rng, T, 2, 8)
+    cu = _cu(lengths)
+    fast = oa.packed_attention(q, k, v, cu, scale=0.3, window=window, causal=causal)
+    slow = oa.brute_force_attention(q, k, v, cu, scale=0.3, window=window, causal=causal)
+    np.testing.assert_allclose(fast, slow, rtol=1e-12, atol=1e-12)
+
+
+def test_single_token_segments_return_v():
+    rng = np.random.default_rng(2)
+    q, k, v = _rand(rng, 6, 3, 16), _rand(rng, 6, 3, 16), _rand(rng, 6, 3, 16)
+    out = oa.packed_attention(q, k, v, _cu([1] * 6), scale=0.125)
+    np.testing.assert_allclose(out, v, rtol=0, atol=1e-12)
+
+
+def test_zero_half_window_and_causal_first_row_return_v():
+    rng = np.random.default_rng(3)
+    q, k, v = _rand(rng, 20, 2, 8), _rand(rng, 20, 2, 8), _rand(rng, 20, 2, 8)
+    cu = _cu([9, 11])
+    out = oa.packed_attention(q, k, v, cu, scale=0.125, window=(0, 0))
+    np.testing.assert_allclose(out, v, atol=1e-12)
+    causal = oa.packed_attention(q, k, v, cu, scale=0.125, causal=True)
+    np.testing.assert_allclose(causal[[0, 9]], v[[0, 9]], atol=1e-12)
+
+
+def test_zero_query_gives_window_mean_of_v():
+    rng = np.random.default_rng(4)
+    L, w = 13, 3
+    q = np.zeros((L, 1, 8), np.float32)
+    k, v = _rand(rng, L, 1, 8), _rand(rng, L, 1, 8)
+    out = oa.packed_attention(q, k, v, _cu([L]), scale=0.125, window=(w, w))
+    for i in range(L):
+        lo, hi = max(0, i - w), min(L, i + w + 1)
+        np.testing.assert_allclose(out[i, 0], v[lo:hi, 0].astype(np.float64).mean(0), atol=1e-12)
+
+
+def test_wide_window_equals_global():
+    rng = np.random.default_rng(5)
+    lengths = [17, 30]
+    T = sum(lengths)
+    q, k, v = _rand(rng, T, 2, 8), _rand(rng, T, 2, 8), _rand(rng, T, 2, 8)
+    cu = _cu(lengths)
+    g = oa.packed_attention(q, k, v, cu, scale=0.2)
+    wide = oa.packed_attention(q, k, v, cu, scale=0.2, window=(29, 29))
+    narrow = oa.packed_attention(q, k, v, cu, scale=0.2, window=(28, 28))
+    np.testing.assert_allclose(wide, g, atol=1e-12)
+    assert np.abs(narrow - g).max() > 1e-6  # the band edge is real
+
+
+def test_gqa_equals_mha_on_repeated_kv_heads():
+    rng = np.random.default_rng(6)
+    lengths = [7, 12]
+    T = sum(lengths)
+    q, k, v = _rand(rng, T, 8, 16), _rand(rng, T, 2, 16), _rand(rng, T, 2, 16)
+    cu = _cu(lengths)
+    gqa = oa.packed_attention(q, k, v, cu, scale=0.25, causal=True)
+    mha = oa.packed_attention(q, np.repeat(k, 4, axis=1), np.repeat(v, 4, axis=1), cu, scale=0.25, causal=True)
+    np.testing.assert_allclose(gqa, mha, atol=1e-12)
+    # head h reads kv head h // 4, not h % 2
+    wrong = oa.packed_attention(q, np.tile(k, (1, 4, 1)), np.tile(v, (1, 4, 1)), cu, scale=0.25, causal=True)
+    assert np.abs(wrong - gqa).max() > 1e-3
+
+
+def test_oracle_matches_torch_sdpa_per_segment():
+    # torch's fp64 SDPA as an independent library routine for the same closed form.
+    rng = np.random.default_rng(7)
+    lengths = [5, 64, 37]
+    T = sum(lengths)
+    q, k, v = _rand(rng, T, 3, 32), _rand(rng, T, 3, 32), _rand(rng, T, 3, 32)
+    cu = _cu(lengths)
+    out = oa.packed_attention(q, k, v, cu, scale=0.17, window=(10, 4))
+    for a, b in zip(cu, cu[1:]):
+        n = b - a
+        qt, kt, vt = (torch.from_numpy(x[a:b]).double().transpose(0, 1) for x in (q, k, v))
+        pos = torch.arange(n)
+        delta = pos[:, None] - pos[None, :]
+        mask = (delta <= 10) & (delta >= -4)
+        ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask, scale=0.17)
+        np.testing.assert_allclose(out[a:b], ref.transpose(0, 1).numpy(), atol=1e-12)
+
+
+def test_sampled_rows_match_full_oracle():
+    rng = np.random.default_rng(8)
+    lengths = [40, 3, 90]
+    T = sum(lengths)
+    q, k, v = _rand(rng, T, 4, 16), _rand(rng, T, 2, 16), _rand(rng, T, 2, 16)
+    cu = _cu(lengths)
+    rows = [0, 39, 40, 42, 43, 100, 132]
+    for window, causal in (((-1, -1), False), ((5, 5), False), ((-1, -1), True)):
+        full = oa.packed_attention(q, k, v, cu, scale=0.25, window=window, causal=causal)
+        part = oa.sampled_rows_attention(q, k, v, cu, rows, scale=0.25, window=window, causal=causal)
+        np.testing.assert_allclose(part, full[rows], atol=1e-12)
+
+
+def test_gate_closed_forms():
+    rng = np.random.default_rng(9)
+    o = oa.to_bf16(_rand(rng, 50, 2, 8))
+    half = oa.sigmoid_gate(o, np.zeros_like(o))  # sigmoid(0) = 0.5 exactly, bf16(o/2) = o/2
+    np.testing.assert_array_equal(half, o.astype(np.float64) / 2)
+    big = oa.sigmoid_gate(o, np.full_like(o, 40.0))  # sigmoid(40) rounds to 1 in bf16
+    np.testing.assert_array_equal(big, o.astype(np.float64))
+    # matches torch's bf16 pipeline: bf16(sigmoid(g)) then bf16(o * s)
+    g = _rand(rng, 50, 2, 8)
+    ot, gt = torch.from_numpy(o).bfloat16(), torch.from_numpy(g)
+    ref = (ot.float() * torch.sigmoid(gt).bfloat16().float()).bfloat16().float().numpy()
+    np.testing.assert_array_equal(oa.sigmoid_gate(o, g).astype(np.float32), ref)
+
+
+def test_allowed_pairs_closed_form(pe):
+    from packed_encoders_amd.hip_attention import allowed_pairs
+
+    for L in (1, 2, 50, 65, 66, 200, 2048):
+        w = 64
+        expected = L * (2 * w + 1) - w * (w + 1) if L > w + 1 else L * L
+        assert allowed_pairs(L, (w, w)) == expected
+        assert allowed_pairs(L) == L * L
+        assert allowed_pairs(L, causal=True) == L * (L + 1) // 2
+        mask = oa.allowed_mask(L, L, (w, w))
+        assert allowed_pairs(L, (w, w)) == int(mask.sum())
