@@ -1,0 +1,352 @@
+#!/usr/bin/env python3
+"""Benchmark of the packed varlen attention path on one MI355X.
+
+Default workload (the one the baseline metric is quoted on): the attention of a ModernBERT-base
+packed batch — 64 documents, lengths LogNormal(400, 0.8) clipped to [32, 2048], 12 heads x 64,
+22 layers (every 3rd global, the rest a +-64 band), bf16. A step is one pass of those 22
+attention calls over synthetic per-layer Q/K/V already resident in HBM, each call the full
+library path (device plan + short kernel + tiled MFMA kernel) through the C ABI on the current
+stream. ``value`` is useful attention TFLOP/s (live token pairs only, ``4*D*H*pairs``).
+
+The dominant kernel (the tiled kernel in the global layers) is bracketed with HIP events on
+its own stream inside the timed region; its algorithmic FLOPs per launch over the average
+launch time give ``roofline.achieved``. The CPU baseline times the same schedule on the host's
+cores with the reference's own CPU kernel (oracle/_ref) for the band and short-global layers
+and per-segment fp32 torch SDPA for global layers longer than 128 (the reference's rule).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "useful attn TFLOP/s & tokens/s, ModernBERT-base packed batch, 1 MI355X; % of roofline"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def compulsory_bytes(total_tokens: int, n_seq: int, hq: int, hkv: int, d: int, gate: bool) -> int:
+    """Read Q, K, V once and write O once (bf16), plus the gate and cu_seqlens."""
+    b = 2 * total_tokens * d * (2 * hq + 2 * hkv) + 4 * (n_seq + 1)
+    if gate:
+        b += 2 * total_tokens * hq * d
+    return b
+
+
+class LayerCall:
+    """One attention call: pre-allocated tensors and C-ABI arguments, launched stage by stage."""
+
+    def __init__(self, lib, hip, workload, layer, cu, q, k, v, gate, short_max):
+        import torch
+
+        self.lib, self.layer = lib, layer
+        self.out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+        self.args = hip._args(q, k, v, self.out, cu, workload.max_seqlen, workload.scale, layer.window[0],
+                              layer.window[1], layer.causal, gate, short_max)
+        size = ctypes.c_size_t()
+        rc = lib.pe_attn_workspace_size(ctypes.byref(self.args), ctypes.byref(size))
+        assert rc == 0, rc
+        self.ws_bytes = size.value
+        self.ws = torch.empty(max(1, size.value), dtype=torch.uint8, device=q.device)
+        self.keep = (q, k, v, gate, cu)
+
+    def short(self, stream):
+        rc = self.lib.pe_attn_short_fwd(ctypes.byref(self.args), stream)
+        if rc:
+            raise RuntimeError(f"pe_attn_short_fwd: {rc}")
+
+    def plan(self, stream):
+        rc = self.lib.pe_attn_plan(ctypes.byref(self.args), self.ws.data_ptr(), self.ws_bytes, stream)
+        if rc:
+            raise RuntimeError(f"pe_attn_plan: {rc}")
+
+    def tiled(self, stream):
+        rc = self.lib.pe_attn_tiled_fwd(ctypes.byref(self.args), self.ws.data_ptr(), self.ws_bytes, stream)
+        if rc:
+            raise RuntimeError(f"pe_attn_tiled_fwd: {rc}")
+
+
+def dominant(workload, short_max):
+    """(stage, bound, layer indices, segments it serves) of the kernel the roofline is for."""
+    long_layers = [i for i, l in enumerate(workload.layers) if l.window == (-1, -1)]
+    if workload.max_seqlen <= short_max:
+        return "short", "hbm", list(range(len(workload.layers)))
+    if long_layers and not any(l.causal or l.gate for l in workload.layers):
+        return "tiled", "mfma", long_layers
+    return "tiled", "hbm", list(range(len(workload.layers)))
+
+
+def gpu_bench(args, workload):
+    import torch
+
+    import packed_encoders_amd as pe
+    from packed_encoders_amd import _lib, hip_attention as hip
+    from packed_encoders_amd.attention_dispatch import hip_short_max
+
+    lib = _lib.library()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    short_max = hip_short_max(workload.head_dim) if args.short_max is None else args.short_max
+    cu = torch.tensor(workload.cu_seqlens(), dtype=torch.int32, device=dev)
+    T, hq, hkv, d = workload.total_tokens, workload.n_heads_q, workload.n_heads_kv, workload.head_dim
+    log(f"{workload.name}: T={T} segments={len(workload.lengths)} max={workload.max_seqlen} heads={hq}/{hkv}x{d} "
+        f"layers={len(workload.layers)} short_max={short_max}")
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    calls = []
+    for layer in workload.layers:
+        q = torch.randn(T, hq, d, device=dev, generator=gen, dtype=torch.bfloat16)
+        k = torch.randn(T, hkv, d, device=dev, generator=gen, dtype=torch.bfloat16)
+        v = torch.randn(T, hkv, d, device=dev, generator=gen, dtype=torch.bfloat16)
+        g = torch.randn(T, hq, d, device=dev, generator=gen, dtype=torch.bfloat16) if layer.gate else None
+        calls.append(LayerCall(lib, hip, workload, layer, cu, q, k, v, g, short_max))
+    stage, bound, timed_layers = dominant(workload, short_max)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    timed_set = set(timed_layers)
+
+    def bracket(fn, events):
+        e0, e1 = events.pop()
+        e0.record(stream)
+        fn(sp)
+        e1.record(stream)
+        timed.append((e0, e1))
+
+    def step(events=None):
+        for i, c in enumerate(calls):
+            here = events is not None and i in timed_set
+            bracket(c.short, events) if here and stage == "short" else c.short(sp)
+            c.plan(sp)
+            bracket(c.tiled, events) if here and stage == "tiled" else c.tiled(sp)
+
+    timed = []
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    pool = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(args.steps * len(timed_layers))]
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g0.record(stream)
+    for _ in range(args.steps):
+        step(pool)
+    g1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall_ms = (t1 - t0) * 1e3 / args.steps
+    gpu_ms = g0.elapsed_time(g1) / args.steps
+    kernel_ms = statistics.mean(a.elapsed_time(b) for a, b in timed)
+
+    # Algorithmic work: all layers for the value; the dominant kernel's own segments for the roofline.
+    flops = sum(hip.useful_flops(workload.lengths, hq, d, window=l.window, causal=l.causal) for l in workload.layers)
+    if stage == "tiled":
+        served = [n for n in workload.lengths if n > short_max]
+    else:
+        served = [n for n in workload.lengths if n <= short_max]
+    layer0 = workload.layers[timed_layers[0]]
+    if bound == "mfma":
+        per_launch = hip.useful_flops(served, hq, d, window=layer0.window, causal=layer0.causal)
+        achieved = per_launch / (kernel_ms * 1e-3) / 1e12
+        peak, unit = PEAK_BF16_TFLOPS, "TFLOP/s"
+    else:
+        per_launch = compulsory_bytes(sum(served), len(served), hq, hkv, d, layer0.gate)
+        achieved = per_launch / (kernel_ms * 1e-3) / 1e9
+        peak, unit = PEAK_HBM_GBS, "GB/s"
+    kernel_name = {"tiled": "tiled_attn_kernel", "short": "short_attn_kernel"}[stage]
+    roofline = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(workload.name, kernel_name),
+                "kernel": kernel_name, "kernel_ms": round(kernel_ms, 4), "algorithmic_per_launch": per_launch}
+    value = flops / (wall_ms * 1e-3) / 1e12
+    sanity_check(calls, workload, cu)
+    log(f"wall {wall_ms:.3f} ms/step (events {gpu_ms:.3f}), {value:.1f} TFLOP/s, dominant {kernel_name} "
+        f"{kernel_ms * 1e3:.1f} us -> {achieved:.1f} {unit} ({achieved / peak:.1%})")
+    return {
+        "value": value, "ms_per_step": wall_ms, "gpu_ms_per_step": gpu_ms, "flops_per_step": flops,
+        "tokens_per_s": workload.total_tokens / (wall_ms * 1e-3), "roofline": roofline, "short_max": short_max,
+    }
+
+
+def sanity_check(calls, workload, cu):
+    """Cheap guard that the timed outputs are real: a sample of rows against the oracle."""
+    import numpy as np
+
+    from oracle import attention as oa
+
+    c = calls[0]
+    q, k, v, gate, _ = c.keep
+    rows = np.linspace(0, workload.total_tokens - 1, 48).astype(np.int64)
+    layer = c.layer
+    want = oa.sampled_rows_attention(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
+                                     cu.cpu().numpy(), rows, scale=workload.scale, window=layer.window,
+                                     causal=layer.causal)
+    got = c.out.float().cpu().numpy()[rows]
+    if gate is not None:
+        want = oa.sigmoid_gate(oa.to_bf16(want), gate.float().cpu().numpy()[rows])
+    err = float(np.abs(got - want).max())
+    if not err <= 2e-2:
+        raise SystemExit(f"bench output check failed: max-abs {err}")
+
+
+def traffic_from_profiles(workload_name: str, kernel: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if one exists."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        table = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = table.get(f"{workload_name}:{kernel}")
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def cpu_threads() -> int:
+    from oracle import cpu
+
+    cores = cpu.physical_cores()
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        cores = min(cores, int(env))
+    return max(1, cores)
+
+
+def cpu_bench(workload, repeats: int = 3):
+    """The same attention schedule on the host CPU (fp32), timed after one warm-up."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from oracle import cpu
+    from packed_encoders_amd import hip_attention as hip
+
+    cpu.build()
+    kind = "reference" if cpu.available("reference") and workload.head_dim == 64 else "port"
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    T, hq, d = workload.total_tokens, workload.n_heads_q, workload.head_dim
+    if workload.n_heads_kv != hq:
+        return None
+    gen = torch.Generator().manual_seed(99)
+    q, k, v = (torch.randn(hq, T, d, generator=gen) for _ in range(3))
+    qn, kn, vn = (t.numpy() for t in (q, k, v))
+    out = np.empty((hq, T, d), dtype=np.float32)
+    lengths = list(workload.lengths)
+    longest = max(lengths)
+    offsets = np.concatenate([[0], np.cumsum(lengths)])
+
+    def layer_call(layer):
+        if layer.causal or layer.gate or layer.window[0] != layer.window[1]:
+            raise ValueError("CPU baseline covers symmetric bands and global attention")
+        if layer.window != (-1, -1):
+            cpu.local_attention(qn, kn, vn, lengths, layer.window[0], kind=kind, threads=threads, out=out,
+                                scale=workload.scale)
+        elif longest <= 128:
+            cpu.local_attention(qn, kn, vn, lengths, longest, kind=kind, threads=threads, out=out,
+                                scale=workload.scale)
+        else:  # per-segment fp32 SDPA, as the reference's CPU engine does for long global layers
+            with torch.inference_mode():
+                for a, b in zip(offsets, offsets[1:]):
+                    F.scaled_dot_product_attention(q[None, :, a:b], k[None, :, a:b], v[None, :, a:b],
+                                                   scale=workload.scale)
+
+    def run():
+        for layer in workload.layers:
+            layer_call(layer)
+
+    run()
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    seconds = statistics.median(times)
+    flops = sum(hip.useful_flops(lengths, hq, d, window=l.window) for l in workload.layers)
+    sample = (f"full {workload.name} schedule ({len(workload.layers)} attention layers, T={T}) in fp32, "
+              f"median of {repeats} after 1 warm-up; band/short layers: "
+              f"{'reference pe_local_attention (oracle/_ref)' if kind == 'reference' else 'oracle C port'}; "
+              f"global layers longer than 128: per-segment torch SDPA")
+    log(f"cpu baseline ({kind}, {threads} threads): {seconds * 1e3:.1f} ms/step -> {flops / seconds / 1e12:.3f} TFLOP/s")
+    return {"value": round(flops / seconds / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": kind,
+            "sample": sample, "ms_per_step": round(seconds * 1e3, 2)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="C2", help="C1 C2 C3 C4 C4-band C5 Q4096 (default C2)")
+    ap.add_argument("--short-max", type=int, default=None, help="routing boundary (default: gfx950 policy)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build runs one MI355X; "
+              "segments shard across GPUs with no exchange, see DESIGN.md", file=sys.stderr)
+        return 2
+
+    import packed_encoders_amd as pe
+
+    w = args.workload
+    workload = {"C1": pe.workloads.c1, "C2": pe.workloads.c2, "C3": pe.workloads.c3, "C4": pe.workloads.c4,
+                "C4-band": lambda: pe.workloads.c4(band=True), "C5": pe.workloads.c5,
+                "Q4096": pe.workloads.query_sweep}[w]()
+    res = gpu_bench(args, workload)
+    cpu_res = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu_res = cpu_bench(workload)
+        except Exception as exc:  # the baseline is reported, never required
+            log(f"cpu baseline skipped: {type(exc).__name__}: {exc}")
+    n_global = sum(1 for l in workload.layers if l.window == (-1, -1))
+    line = {
+        "metric": METRIC,
+        "value": round(res["value"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": workload.name + ": " + workload.description,
+            "n_segments": len(workload.lengths),
+            "total_tokens": workload.total_tokens,
+            "max_seqlen": workload.max_seqlen,
+            "heads_q": workload.n_heads_q,
+            "heads_kv": workload.n_heads_kv,
+            "head_dim": workload.head_dim,
+            "attention_layers": len(workload.layers),
+            "global_layers": n_global,
+            "short_max": res["short_max"],
+            "parallelism": "single GPU",
+        },
+        "tokens_per_s": round(res["tokens_per_s"], 1),
+        "gpu_ms_per_step": round(res["gpu_ms_per_step"], 4),
+        "roofline": res["roofline"],
+        "cpu_baseline": cpu_res,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -71,8 +71,8 @@ typedef struct pe_attn_args {
     int32_t causal;       /* 0 or 1; causal is window_right = 0 */
     /* Per-segment routing: segments with length <= short_max run the LDS-resident short
        kernel, longer ones the tiled MFMA kernel. 0 sends every segment to the tiled kernel;
-       -1 asks for the library's gfx950 default. At most 128 (64 for head_dim 256 is refused:
-       the short kernel covers head_dim <= 128). */
+       -1 asks for the library's gfx950 default. At most 128; head_dim 256 always runs the
+       tiled kernel (the short kernel covers head_dim <= 128). */
     int32_t short_max;
 } pe_attn_args;
 
@@ -95,6 +95,19 @@ int pe_attn_workspace_size(const pe_attn_args *args, size_t *bytes);
    gate (packed_encoders/_kernels/hybrid.py:197-219) included. */
 int pe_varlen_attn_fwd(const pe_attn_args *args, void *workspace, size_t workspace_bytes,
                        hipStream_t stream);
+
+/* The three stages pe_varlen_attn_fwd runs, for callers that reuse one plan across calls
+   (the 22 layers of a packed forward share cu_seqlens: one plan per window kind serves all
+   of them) or time one kernel. A plan is valid for arguments with the same cu_seqlens
+   contents, n_seq, total_tokens, max_seqlen, head counts, window, causal and short_max.
+   pe_attn_plan: build the cost-ordered (segment, query tile) list of the tiled kernel into
+     the workspace (no-op when no segment can exceed short_max).
+   pe_attn_short_fwd: the short kernel over segments with length <= short_max (no-op for 0).
+   pe_attn_tiled_fwd: the tiled kernel over a planned workspace. */
+int pe_attn_plan(const pe_attn_args *args, void *workspace, size_t workspace_bytes, hipStream_t stream);
+int pe_attn_short_fwd(const pe_attn_args *args, hipStream_t stream);
+int pe_attn_tiled_fwd(const pe_attn_args *args, const void *workspace, size_t workspace_bytes,
+                      hipStream_t stream);
 
 /* Packed short attention: every segment through the LDS-resident short kernel. Requires
    0 < max_seqlen <= 128 and head_dim <= 128; short_max is ignored. Needs no workspace.

@@ -17,7 +17,7 @@ repository root) is its importable alias.
 from __future__ import annotations
 
 from . import errors, workloads
-from . import _lib, hip_attention
+from . import _lib, attention_dispatch, hip_attention
 from .errors import PackedEncodersError, UnsupportedTargetError, ValidationError
 from .hip_attention import (
     packed_short_attention,

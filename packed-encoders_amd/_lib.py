@@ -22,6 +22,9 @@ EXPORTED = (
     "pe_attn_strerror",
     "pe_attn_workspace_size",
     "pe_varlen_attn_fwd",
+    "pe_attn_plan",
+    "pe_attn_short_fwd",
+    "pe_attn_tiled_fwd",
     "pe_packed_short_attn_fwd",
     "pe_attn_short_config",
 )
@@ -83,6 +86,12 @@ def library(path: str | None = None) -> ctypes.CDLL:
     lib.pe_attn_workspace_size.argtypes = [ctypes.POINTER(AttnArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.pe_varlen_attn_fwd.restype = ctypes.c_int
     lib.pe_varlen_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.pe_attn_plan.restype = ctypes.c_int
+    lib.pe_attn_plan.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.pe_attn_short_fwd.restype = ctypes.c_int
+    lib.pe_attn_short_fwd.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p]
+    lib.pe_attn_tiled_fwd.restype = ctypes.c_int
+    lib.pe_attn_tiled_fwd.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.pe_packed_short_attn_fwd.restype = ctypes.c_int
     lib.pe_packed_short_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p]
     lib.pe_attn_short_config.restype = ctypes.c_int

@@ -175,6 +175,30 @@ int launch_tiled(const AttnParams &p, int d, int g, bool gate, int64_t cap, hipS
 
 constexpr size_t kWorkspaceHeader = 256;  // the entry count lives here, list follows aligned
 
+// Workspace layout: [0, 256) header (int32 entry count), then the (segment, tile) list.
+struct Plan {
+    int sm, g, bm;
+    int64_t cap;
+};
+
+int prepare(const pe_attn_args *a, Plan *plan) {
+    int rc = check_args(a);
+    if (rc) return rc;
+    plan->sm = effective_short_max(a);
+    plan->g = heads_per_tile(a);
+    plan->bm = 32 * (4 / plan->g);
+    plan->cap = tile_capacity(a, plan->sm, plan->bm);
+    if (plan->cap > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
+    return PE_ATTN_OK;
+}
+
+int check_workspace(const Plan &plan, const void *workspace, size_t bytes) {
+    if (plan.cap > 0 && (!workspace || !aligned16(workspace) ||
+                         bytes < kWorkspaceHeader + (size_t)plan.cap * sizeof(int2)))
+        return PE_ATTN_EWORKSPACE;
+    return PE_ATTN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -203,36 +227,52 @@ int pe_attn_workspace_size(const pe_attn_args *a, size_t *bytes) {
     return PE_ATTN_OK;
 }
 
-int pe_varlen_attn_fwd(const pe_attn_args *a, void *workspace, size_t workspace_bytes, hipStream_t stream) {
-    int rc = check_args(a);
+int pe_attn_plan(const pe_attn_args *a, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    Plan plan;
+    int rc = prepare(a, &plan);
     if (rc) return rc;
-    if (a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
-    const int sm = effective_short_max(a);
-    const int g = heads_per_tile(a);
-    const int bm = 32 * (4 / g);
-    const int64_t cap = tile_capacity(a, sm, bm);
-    if (cap > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
-    if (cap > 0 && (!workspace || !aligned16(workspace) ||
-                    workspace_bytes < kWorkspaceHeader + (size_t)cap * sizeof(int2)))
-        return PE_ATTN_EWORKSPACE;
-    AttnParams p = make_params(a, sm);
-    const bool gate = a->gate != nullptr;
-    if (sm > 0) {
-        rc = launch_short(p, a->head_dim, gate, sm, stream);
-        if (rc) return rc;
-    }
-    if (cap > 0) {
-        int32_t *count = static_cast<int32_t *>(workspace);
-        int2 *work = reinterpret_cast<int2 *>(static_cast<char *>(workspace) + kWorkspaceHeader);
-        hipLaunchKernelGGL(pe::plan_kernel, dim3(1), dim3(1024), 0, stream, a->cu_seqlens, a->n_seq, sm, bm,
-                           p.wl, p.wr, work, count, (int)cap);
-        if (hipGetLastError() != hipSuccess) return PE_ATTN_ELAUNCH;
-        p.work = work;
-        p.work_count = count;
-        rc = launch_tiled(p, a->head_dim, g, gate, cap, stream);
-        if (rc) return rc;
-    }
-    return PE_ATTN_OK;
+    if (plan.cap == 0) return PE_ATTN_OK;
+    rc = check_workspace(plan, workspace, workspace_bytes);
+    if (rc) return rc;
+    int32_t *count = static_cast<int32_t *>(workspace);
+    int2 *work = reinterpret_cast<int2 *>(static_cast<char *>(workspace) + kWorkspaceHeader);
+    const int wr = a->causal ? 0 : a->window_right;
+    hipLaunchKernelGGL(pe::plan_kernel, dim3(1), dim3(1024), 0, stream, a->cu_seqlens, a->n_seq, plan.sm, plan.bm,
+                       a->window_left, wr, work, count, (int)plan.cap);
+    return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
+}
+
+int pe_attn_short_fwd(const pe_attn_args *a, hipStream_t stream) {
+    Plan plan;
+    const int rc = prepare(a, &plan);
+    if (rc) return rc;
+    if (plan.sm == 0 || a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
+    const AttnParams p = make_params(a, plan.sm);
+    return launch_short(p, a->head_dim, a->gate != nullptr, plan.sm, stream);
+}
+
+int pe_attn_tiled_fwd(const pe_attn_args *a, const void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    Plan plan;
+    int rc = prepare(a, &plan);
+    if (rc) return rc;
+    if (plan.cap == 0) return PE_ATTN_OK;
+    rc = check_workspace(plan, workspace, workspace_bytes);
+    if (rc) return rc;
+    AttnParams p = make_params(a, plan.sm);
+    p.work_count = static_cast<const int32_t *>(workspace);
+    p.work = reinterpret_cast<const int2 *>(static_cast<const char *>(workspace) + kWorkspaceHeader);
+    return launch_tiled(p, a->head_dim, plan.g, a->gate != nullptr, plan.cap, stream);
+}
+
+int pe_varlen_attn_fwd(const pe_attn_args *a, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    Plan plan;
+    int rc = prepare(a, &plan);
+    if (rc) return rc;
+    rc = check_workspace(plan, workspace, workspace_bytes);
+    if (rc) return rc;
+    if ((rc = pe_attn_short_fwd(a, stream))) return rc;
+    if ((rc = pe_attn_plan(a, workspace, workspace_bytes, stream))) return rc;
+    return pe_attn_tiled_fwd(a, workspace, workspace_bytes, stream);
 }
 
 int pe_packed_short_attn_fwd(const pe_attn_args *a, hipStream_t stream) {

@@ -45,9 +45,11 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
     if (entry >= *p.work_count) return;
     const int2 w = p.work[entry];
     const int seg = w.x, tile = w.y;
+    if (seg < 0 || seg >= p.n_seq || tile < 0) return;  // a plan made for other arguments
     const int start = p.cu[seg];
     const int L = p.cu[seg + 1] - start;
     const int q0 = tile * BM;
+    if (q0 >= L) return;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, kg = lane >> 5;
