@@ -27,6 +27,9 @@ HIPCC_FLAGS = [
     "-shared",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep MFMA accumulators in ordinary VGPRs: the softmax reads every score element, and
+    # AGPR-resident accumulators would cost a v_accvgpr_read per element and per rescale
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 SOURCES = ["pe_attn_capi.hip"]
 

@@ -58,6 +58,14 @@ int check_args(const pe_attn_args *a, bool need_pointers = true) {
             (a->gate_stride_token & 7) || (a->gate_stride_head & 7))
             return PE_ATTN_EINVAL;
     }
+    // Kernels address a segment through 32-bit buffer offsets bounded by its last row: rows
+    // must not overlap (token stride >= head_dim) and a segment must span < 2 GiB per tensor.
+    const int64_t token_strides[5] = {a->q_stride_token, a->k_stride_token, a->v_stride_token, a->o_stride_token,
+                                      a->gate ? a->gate_stride_token : a->head_dim};
+    for (int64_t s : token_strides) {
+        if (a->total_tokens > 1 && s < a->head_dim) return PE_ATTN_EINVAL;
+        if ((int64_t)a->max_seqlen * s * 2 + 2 * a->head_dim >= (int64_t)1 << 31) return PE_ATTN_EUNSUPPORTED;
+    }
     return PE_ATTN_OK;
 }
 

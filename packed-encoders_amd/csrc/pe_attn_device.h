@@ -46,6 +46,40 @@ struct AttnParams {
     const int32_t *work_count; // tiled kernel: number of valid entries
 };
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// Buffer resources. A raw buffer (stride 0) whose range ends at the last byte of a segment's
+// last row makes the hardware return 0 for any load beyond it and drop any store beyond it,
+// so segment tails need no branches; offsets are 32-bit (voffset VGPR + soffset SGPR).
+// Word 3 is the gfx9 raw-buffer configuration (32-bit data format, no swizzle).
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, kBufferWord3);
+}
+
+// Range of `rows` rows of `d` bf16 elements `stride` elements apart (0 rows: empty range).
+__device__ __forceinline__ uint32_t rows_bytes(int rows, int64_t stride, int d) {
+    return rows > 0 ? (uint32_t)((int64_t)(rows - 1) * stride * 2 + d * 2) : 0u;
+}
+
+__device__ __forceinline__ bf16x8 buf_ld16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ bf16x4 buf_ld8(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+__device__ __forceinline__ void buf_st8(__amdgpu_buffer_rsrc_t r, int voff, bf16x4 x) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, x), r, voff, 0, 0);
+}
+
+// Wave-uniform value as a scalar (lets the compiler branch on SCC instead of EXEC masks).
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// True when `pred` holds on any lane of the wave (a scalar result).
+__device__ __forceinline__ bool wave_any(bool pred) { return __builtin_amdgcn_ballot_w64(pred) != 0; }
+
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -113,6 +147,26 @@ __device__ __forceinline__ bool block_full(int kb0, int L, int r0, int r1, int w
     if (wl >= 0 && (r1 - 1) - kb0 > wl) return false;
     if (wr >= 0 && (kb0 + 31) - r0 > wr) return false;
     return true;
+}
+
+// Round 4 fp32 outputs to bf16 and apply the optional fused sigmoid gate (g holds the gate's
+// 4 bf16 values): y = bf16(bf16(o) * bf16(sigmoid(g))), the rounding order of the reference's
+// gate kernel (packed_encoders/_kernels/hybrid.py:197-206).
+template <bool GATE>
+__device__ __forceinline__ bf16x4 out4(float a0, float a1, float a2, float a3, bf16x4 g) {
+    bf16x4 r;
+    r[0] = (__bf16)a0;
+    r[1] = (__bf16)a1;
+    r[2] = (__bf16)a2;
+    r[3] = (__bf16)a3;
+    if constexpr (GATE) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float sg = (float)(__bf16)(1.0f / (1.0f + __expf(-(float)g[i])));
+            r[i] = (__bf16)((float)r[i] * sg);
+        }
+    }
+    return r;
 }
 
 // Store 4 consecutive output dims of one row, with the optional fused sigmoid gate:
