@@ -136,23 +136,23 @@ void short_shape(int max_len, int d, int *sk, int *hpw) {
 }
 
 template <int D, bool GATE>
-int launch_short_d(const AttnParams &p, int sk, int hpw, hipStream_t stream) {
-    if (D == 64) {
+int launch_short_d(const AttnParams &p, int sk, hipStream_t stream) {
+    if constexpr (D == 64) {
         if (sk == 32) return launch_short_t<D, 32, 4, GATE>(p, stream);
         if (sk == 64) return launch_short_t<D, 64, 4, GATE>(p, stream);
         return launch_short_t<D, 128, 2, GATE>(p, stream);
+    } else {
+        if (sk == 32) return launch_short_t<D, 32, 4, GATE>(p, stream);
+        if (sk == 64) return launch_short_t<D, 64, 2, GATE>(p, stream);
+        return launch_short_t<D, 128, 1, GATE>(p, stream);
     }
-    if (sk == 32) return launch_short_t<D, 32, 4, GATE>(p, stream);
-    if (sk == 64) return launch_short_t<D, 64, 2, GATE>(p, stream);
-    return launch_short_t<D, 128, 1, GATE>(p, stream);
-    (void)hpw;
 }
 
 int launch_short(const AttnParams &p, int d, bool gate, int short_max, hipStream_t stream) {
     int sk, hpw;
     short_shape(short_max, d, &sk, &hpw);
-    if (d == 64) return gate ? launch_short_d<64, true>(p, sk, hpw, stream) : launch_short_d<64, false>(p, sk, hpw, stream);
-    if (d == 128) return gate ? launch_short_d<128, true>(p, sk, hpw, stream) : launch_short_d<128, false>(p, sk, hpw, stream);
+    if (d == 64) return gate ? launch_short_d<64, true>(p, sk, stream) : launch_short_d<64, false>(p, sk, stream);
+    if (d == 128) return gate ? launch_short_d<128, true>(p, sk, stream) : launch_short_d<128, false>(p, sk, stream);
     return PE_ATTN_EUNSUPPORTED;
 }
 

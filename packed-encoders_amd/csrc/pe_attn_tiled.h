@@ -101,12 +101,15 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
     const int voff = vkq * KQ * v_row + vdc * 16;
     const int vlds = (vdc * 8) * VP + vperm(vkq * KQ);
 
+    // The tile offset goes into the VGPR offset, never the SGPR one: only the former is
+    // guaranteed to take part in the buffer range check that zeroes rows past the segment.
     bf16x8 kreg[KQ], vreg[KQ];
     auto gload = [&](int kt0) {
+        const int kbase = kt0 * k_row, vbase = kt0 * v_row;
 #pragma unroll
-        for (int i = 0; i < KQ; ++i) kreg[i] = buf_ld16(k_rs, koff[i], kt0 * k_row);
+        for (int i = 0; i < KQ; ++i) kreg[i] = buf_ld16(k_rs, koff[i] + kbase, 0);
 #pragma unroll
-        for (int r = 0; r < KQ; ++r) vreg[r] = buf_ld16(v_rs, voff, (kt0 + r) * v_row);
+        for (int r = 0; r < KQ; ++r) vreg[r] = buf_ld16(v_rs, voff + vbase + r * v_row, 0);
     };
     auto swrite = [&](int buf) {
 #pragma unroll
