@@ -285,6 +285,25 @@ def cpu_bench(workload, repeats: int = 3):
             "sample": sample, "ms_per_step": round(seconds * 1e3, 2)}
 
 
+def copy_calibration(steps: int) -> int:
+    """A plain device copy of known size: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this run,
+    divided by the bytes moved, is the factor that turns those counters into HBM bytes."""
+    import torch
+
+    n = 1 << 30
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / max(1, steps)
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": steps,
+                      "ms_per_copy": round(dt * 1e3, 4), "GBps_read_plus_write": round(2 * n / dt / 1e9, 1)}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -293,11 +312,16 @@ def main() -> int:
     ap.add_argument("--workload", default="C2", help="C1 C2 C3 C4 C4-band C5 Q4096 (default C2)")
     ap.add_argument("--short-max", type=int, default=None, help="routing boundary (default: gfx950 policy)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy a 1 GiB buffer --steps times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build runs one MI355X; "
               "segments shard across GPUs with no exchange, see DESIGN.md", file=sys.stderr)
         return 2
+
+    if args.copy_calibration:
+        return copy_calibration(args.steps)
 
     import packed_encoders_amd as pe
 

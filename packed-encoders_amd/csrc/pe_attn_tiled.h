@@ -147,6 +147,13 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
         swrite(0);
     }
     __syncthreads();
+    // The query fragments arrived before tile 0 (issued earlier, and loads complete in
+    // order). Re-defining them through an empty asm ends their load's scope here: otherwise
+    // the compiler, seeing them possibly in flight at the loop header, waits on the vector
+    // memory counter before the first MFMA of every tile, which also drains the next
+    // tile's prefetch and serialises the double buffer.
+#pragma unroll
+    for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[c]));
 
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
