@@ -5,14 +5,18 @@ Default workload (the one the baseline metric is quoted on): the attention of a 
 packed batch — 64 documents, lengths LogNormal(400, 0.8) clipped to [32, 2048], 12 heads x 64,
 22 layers (every 3rd global, the rest a +-64 band), bf16. A step is one pass of those 22
 attention calls over synthetic per-layer Q/K/V already resident in HBM, each call the full
-library path (device plan + short kernel + tiled MFMA kernel) through the C ABI on the current
-stream. ``value`` is useful attention TFLOP/s (live token pairs only, ``4*D*H*pairs``).
+library path through the C ABI on the current stream: the short kernel and the tiled MFMA
+kernel per layer, plus one device-built tile plan per window kind (global, +-64), which every
+layer of that kind shares as a packed forward does. ``value`` is useful attention TFLOP/s
+(live token pairs only, ``4*D*H*pairs``); ``tokens_per_s`` is packed tokens through all 22
+attention layers per second.
 
-The dominant kernel (the tiled kernel in the global layers) is bracketed with HIP events on
-its own stream inside the timed region; its algorithmic FLOPs per launch over the average
-launch time give ``roofline.achieved``. The CPU baseline times the same schedule on the host's
-cores with the reference's own CPU kernel (oracle/_ref) for the band and short-global layers
-and per-segment fp32 torch SDPA for global layers longer than 128 (the reference's rule).
+The dominant kernel (the tiled kernel of the global layers) is bracketed with HIP events
+recorded on the stream it is launched on, inside the timed region; its algorithmic FLOPs per
+launch over the average launch time give ``roofline.achieved``. The CPU baseline times the same
+schedule on the host's cores with the reference's own CPU kernel (oracle/_ref) for the band and
+short-global layers and per-segment fp32 torch SDPA for global layers longer than 128 (the
+reference's rule).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2] [--no-cpu-baseline]
 """
@@ -22,6 +26,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import statistics
 import sys
@@ -50,9 +55,13 @@ def compulsory_bytes(total_tokens: int, n_seq: int, hq: int, hkv: int, d: int, g
 
 
 class LayerCall:
-    """One attention call: pre-allocated tensors and C-ABI arguments, launched stage by stage."""
+    """One attention call: pre-allocated tensors and C-ABI arguments, launched stage by stage.
 
-    def __init__(self, lib, hip, workload, layer, cu, q, k, v, gate, short_max):
+    Layers with the same window kind share one tile plan (workspace): the plan depends only on
+    cu_seqlens, the window and the head geometry, so a packed forward builds it once per kind
+    (twice for ModernBERT: global and +-64) and every layer of that kind reuses it."""
+
+    def __init__(self, lib, hip, workload, layer, cu, q, k, v, gate, short_max, plans):
         import torch
 
         self.lib, self.layer = lib, layer
@@ -63,7 +72,11 @@ class LayerCall:
         rc = lib.pe_attn_workspace_size(ctypes.byref(self.args), ctypes.byref(size))
         assert rc == 0, rc
         self.ws_bytes = size.value
-        self.ws = torch.empty(max(1, size.value), dtype=torch.uint8, device=q.device)
+        kind = (layer.window, layer.causal)
+        self.plans_here = kind not in plans  # the first layer of a kind builds the shared plan
+        if self.plans_here:
+            plans[kind] = torch.empty(max(1, size.value), dtype=torch.uint8, device=q.device)
+        self.ws = plans[kind]
         self.keep = (q, k, v, gate, cu)
 
     def short(self, stream):
@@ -83,13 +96,28 @@ class LayerCall:
 
 
 def dominant(workload, short_max):
-    """(stage, bound, layer indices, segments it serves) of the kernel the roofline is for."""
-    long_layers = [i for i, l in enumerate(workload.layers) if l.window == (-1, -1)]
+    """(stage, bound, layer indices) of the kernel the roofline is for: the tiled kernel of the
+    global layers when there are any (MFMA-bound), else the kernel of the windowed/causal
+    layers (HBM-bound), or the short kernel when every segment is short."""
+    long_layers = [i for i, l in enumerate(workload.layers) if l.window == (-1, -1) and not l.causal]
     if workload.max_seqlen <= short_max:
         return "short", "hbm", list(range(len(workload.layers)))
-    if long_layers and not any(l.causal or l.gate for l in workload.layers):
+    if long_layers and not any(l.gate for l in workload.layers):
         return "tiled", "mfma", long_layers
     return "tiled", "hbm", list(range(len(workload.layers)))
+
+
+def kernel_instance(stage, workload, layer, short_max):
+    """The kernel's name as rocprofv3 lists it (template arguments included)."""
+    d = workload.head_dim
+    if stage == "short":
+        sk = 32 if short_max <= 32 else (64 if short_max <= 64 else 128)
+        hpw = (2 if sk == 128 else 4) if d == 64 else (4 if sk == 32 else (2 if sk == 64 else 1))
+        return f"pe::short_attn_kernel<{d}, {sk}, {hpw}, {str(layer.gate).lower()}>"
+    g = math.gcd(workload.n_heads_q // workload.n_heads_kv, 4)
+    bn = 32 if d >= 256 else 64
+    win = layer.window != (-1, -1) or layer.causal
+    return f"pe::tiled_attn_kernel<{d}, {g}, {bn}, {str(layer.gate).lower()}, {str(win).lower()}>"
 
 
 def gpu_bench(args, workload):
@@ -108,13 +136,13 @@ def gpu_bench(args, workload):
     log(f"{workload.name}: T={T} segments={len(workload.lengths)} max={workload.max_seqlen} heads={hq}/{hkv}x{d} "
         f"layers={len(workload.layers)} short_max={short_max}")
     gen = torch.Generator(device=dev).manual_seed(1234)
-    calls = []
+    calls, plans = [], {}
     for layer in workload.layers:
         q = torch.randn(T, hq, d, device=dev, generator=gen, dtype=torch.bfloat16)
         k = torch.randn(T, hkv, d, device=dev, generator=gen, dtype=torch.bfloat16)
         v = torch.randn(T, hkv, d, device=dev, generator=gen, dtype=torch.bfloat16)
         g = torch.randn(T, hq, d, device=dev, generator=gen, dtype=torch.bfloat16) if layer.gate else None
-        calls.append(LayerCall(lib, hip, workload, layer, cu, q, k, v, g, short_max))
+        calls.append(LayerCall(lib, hip, workload, layer, cu, q, k, v, g, short_max, plans))
     stage, bound, timed_layers = dominant(workload, short_max)
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
@@ -132,7 +160,8 @@ def gpu_bench(args, workload):
         for i, c in enumerate(calls):
             here = events is not None and i in timed_set
             bracket(c.short, events) if here and stage == "short" else c.short(sp)
-            c.plan(sp)
+            if c.plans_here:
+                c.plan(sp)
             bracket(c.tiled, events) if here and stage == "tiled" else c.tiled(sp)
 
     timed = []
@@ -169,7 +198,7 @@ def gpu_bench(args, workload):
         per_launch = compulsory_bytes(sum(served), len(served), hq, hkv, d, layer0.gate)
         achieved = per_launch / (kernel_ms * 1e-3) / 1e9
         peak, unit = PEAK_HBM_GBS, "GB/s"
-    kernel_name = {"tiled": "tiled_attn_kernel", "short": "short_attn_kernel"}[stage]
+    kernel_name = kernel_instance(stage, workload, layer0, short_max)
     roofline = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                 "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(workload.name, kernel_name),
                 "kernel": kernel_name, "kernel_ms": round(kernel_ms, 4), "algorithmic_per_launch": per_launch}

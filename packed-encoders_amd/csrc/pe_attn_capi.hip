@@ -156,28 +156,35 @@ int launch_short(const AttnParams &p, int d, bool gate, int short_max, hipStream
     return PE_ATTN_EUNSUPPORTED;
 }
 
-template <int D, int G, bool GATE>
+template <int D, int G, bool GATE, bool WIN>
 int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
     constexpr int BN = D >= 256 ? 32 : 64;
     p.hgroups = p.hq / G;
     const int64_t blocks = cap * p.hgroups;
     if (blocks <= 0) return PE_ATTN_OK;
     if (blocks > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
-    hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, GATE>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
     return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
 }
 
-template <int D, bool GATE>
-int launch_tiled_d(const AttnParams &p, int g, int64_t cap, hipStream_t stream) {
-    if (g == 4) return launch_tiled_t<D, 4, GATE>(p, cap, stream);
-    if (g == 2) return launch_tiled_t<D, 2, GATE>(p, cap, stream);
-    return launch_tiled_t<D, 1, GATE>(p, cap, stream);
+template <int D, bool GATE, bool WIN>
+int launch_tiled_g(const AttnParams &p, int g, int64_t cap, hipStream_t stream) {
+    if (g == 4) return launch_tiled_t<D, 4, GATE, WIN>(p, cap, stream);
+    if (g == 2) return launch_tiled_t<D, 2, GATE, WIN>(p, cap, stream);
+    return launch_tiled_t<D, 1, GATE, WIN>(p, cap, stream);
+}
+
+template <int D>
+int launch_tiled_d(const AttnParams &p, int g, bool gate, int64_t cap, hipStream_t stream) {
+    const bool win = p.wl >= 0 || p.wr >= 0;
+    if (gate) return win ? launch_tiled_g<D, true, true>(p, g, cap, stream) : launch_tiled_g<D, true, false>(p, g, cap, stream);
+    return win ? launch_tiled_g<D, false, true>(p, g, cap, stream) : launch_tiled_g<D, false, false>(p, g, cap, stream);
 }
 
 int launch_tiled(const AttnParams &p, int d, int g, bool gate, int64_t cap, hipStream_t stream) {
-    if (d == 64) return gate ? launch_tiled_d<64, true>(p, g, cap, stream) : launch_tiled_d<64, false>(p, g, cap, stream);
-    if (d == 128) return gate ? launch_tiled_d<128, true>(p, g, cap, stream) : launch_tiled_d<128, false>(p, g, cap, stream);
-    if (d == 256) return gate ? launch_tiled_d<256, true>(p, g, cap, stream) : launch_tiled_d<256, false>(p, g, cap, stream);
+    if (d == 64) return launch_tiled_d<64>(p, g, gate, cap, stream);
+    if (d == 128) return launch_tiled_d<128>(p, g, gate, cap, stream);
+    if (d == 256) return launch_tiled_d<256>(p, g, gate, cap, stream);
     return PE_ATTN_EUNSUPPORTED;
 }
 

@@ -14,8 +14,9 @@
 //
 // Softmax: online, fp32, log2 domain. The running maximum is raised lazily — only when a new
 // tile's maximum exceeds it by more than 2^8 on some lane of the wave — so the accumulator
-// rescale is skipped on almost every tile; numerator and denominator always share the stale
-// maximum, so the result is the same up to rounding. Probabilities are rounded to bf16 for the
+// rescale (and the exchange of maxima between the two lanes of a query row) is skipped on
+// almost every tile; numerator and denominator always share the stale maximum, so the result
+// is the same up to rounding. Probabilities are rounded to bf16 for the
 // P.V MFMA (the reference's precision strategy,
 // packed_encoders/_kernels/triton_packed_attention.py:122-136).
 //
@@ -30,7 +31,10 @@ namespace pe {
 
 constexpr float kLazyRescale = 8.0f;  // log2 of the largest unnormalised probability allowed
 
-template <int D, int G, int BN, bool GATE>
+// WIN: the call has a window or causal bound. Without one (global attention) every window
+// test folds away at compile time, which also gives global and windowed launches distinct
+// kernel names in traces.
+template <int D, int G, int BN, bool GATE, bool WIN>
 __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
     static_assert(D % 32 == 0 && BN % 32 == 0 && (4 % G) == 0, "tile shape");
     constexpr int WPH = 4 / G;       // waves per query head
@@ -67,7 +71,7 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
     const int kvh = (hg * G) / p.group;
     const int r0 = q0 + rb * 32;
     const int myrow = r0 + col;
-    const int wl = p.wl, wr = p.wr;
+    const int wl = WIN ? p.wl : -1, wr = WIN ? p.wr : -1;
 
     const int rows_end = min(L, q0 + BM);
     const int klo = wl >= 0 ? max(0, q0 - wl) : 0;
@@ -138,7 +142,10 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
     for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int j = 0; j < 16; ++j) o[db][j] = 0.0f;
-    float m = kNegInf, lsum = 0.0f;
+    // Running maximum (log2 domain) and row sum; the sum is kept as 4 partial sums so the
+    // 16 additions of a block form 4 independent chains instead of one serial chain.
+    float m = kNegInf;
+    float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const float c2 = p.c;
 
     const int ntiles = khi > klo ? (khi - klo + BN - 1) / BN : 0;
@@ -163,7 +170,7 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
         if (wave_active) {
             f32x16 s[NB];
             bool live[NB];
-            float mx = kNegInf;
+            float mp[4] = {kNegInf, kNegInf, kNegInf, kNegInf};  // partial maxima (4 chains)
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const int kb0 = kt0 + 32 * b;
@@ -185,16 +192,18 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
                     }
                     s[b] = acc;
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, acc[j]);
+                    for (int j = 0; j < 16; ++j) mp[j & 3] = fmaxf(mp[j & 3], acc[j]);
                 }
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mxt = mx * c2;
-            if (wave_any(mxt > m + kLazyRescale)) {
-                const float mnew = fmaxf(m, mxt);
+            // Each lane tests its own maximum: the two lanes of a query row share m, so "some
+            // lane exceeds m" is "some row exceeds m"; only a rescale combines the pair.
+            const float mx = fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]));
+            if (wave_any(mx * c2 > m + kLazyRescale)) {
+                const float mnew = fmaxf(m, fmaxf(mx, __shfl_xor(mx, 32)) * c2);
                 const float alpha = mnew == kNegInf ? 1.0f : exp2_fast(m - mnew);
                 m = mnew;
-                lsum *= alpha;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ls[i] *= alpha;
 #pragma unroll
                 for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -208,7 +217,7 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
                     for (int j = 0; j < 16; ++j) {
                         const float e = exp2_fast(fmaf(s[b][j], c2, -muse));
                         s[b][j] = e;
-                        lsum += e;
+                        ls[j & 3] += e;
                     }
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
@@ -224,6 +233,7 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
         __syncthreads();
     }
 
+    const float lsum = (ls[0] + ls[1]) + (ls[2] + ls[3]);
     const float lt = lsum + __shfl_xor(lsum, 32);
     if (!wave_active) return;
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
