@@ -14,6 +14,8 @@ CPU or eager-PyTorch fallback: if the library is missing, the loader raises ``Im
 
 from __future__ import annotations
 
+import contextlib
+import contextvars
 import ctypes
 
 import torch
@@ -79,6 +81,29 @@ def _check_tensors(q: Tensor, k: Tensor, v: Tensor, cu: Tensor, gate: Tensor | N
         raise ValueError("q, k, v, cu_seqlens (and gate) must be on one HIP device")
 
 
+# Tile plans shared within a scope (one packed forward): key -> (cu_seqlens, workspace, bytes).
+_PLANS: contextvars.ContextVar[dict | None] = contextvars.ContextVar("pe_hip_shared_plans", default=None)
+
+
+@contextlib.contextmanager
+def shared_plans():
+    """Within this scope, varlen attention calls that share a ``cu_seqlens`` tensor, head
+    geometry, window, causality and routing boundary build the tiled kernel's plan once and
+    reuse it: a packed forward's 22 layers then run 2 plan kernels (global and local) instead
+    of 22. The scope keeps each plan's workspace (and its ``cu_seqlens``) alive until it exits;
+    the caller must not change ``cu_seqlens`` values inside the scope."""
+    token = _PLANS.set({})
+    try:
+        yield
+    finally:
+        _PLANS.reset(token)
+
+
+def _plan_key(args: _lib.AttnArgs, cu: Tensor) -> tuple:
+    return (id(cu), cu.data_ptr(), cu.numel(), args.total_tokens, args.max_seqlen, args.n_heads_q,
+            args.n_heads_kv, args.head_dim, args.window_left, args.window_right, args.causal, args.short_max)
+
+
 def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int,
                  softmax_scale: float, window_left: int, window_right: int, causal: bool,
                  gate: Tensor | None, short_max: int) -> Tensor:
@@ -91,13 +116,29 @@ def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen
     lib = _lib.library()
     args = _args(q, k, v, out, cu_seqlens, max_seqlen, softmax_scale, window_left, window_right,
                  causal, gate, short_max)
-    size = ctypes.c_size_t(0)
-    _lib.check(lib.pe_attn_workspace_size(ctypes.byref(args), ctypes.byref(size)), "pe_attn_workspace_size")
-    workspace = torch.empty(size.value, dtype=torch.uint8, device=q.device) if size.value else None
     stream = torch.cuda.current_stream(q.device).cuda_stream
-    status = lib.pe_varlen_attn_fwd(ctypes.byref(args), workspace.data_ptr() if workspace is not None else None,
-                                    size.value, stream)
-    _lib.check(status, "pe_varlen_attn_fwd")
+    plans = _PLANS.get()
+    if plans is None:
+        size = ctypes.c_size_t(0)
+        _lib.check(lib.pe_attn_workspace_size(ctypes.byref(args), ctypes.byref(size)), "pe_attn_workspace_size")
+        workspace = torch.empty(size.value, dtype=torch.uint8, device=q.device) if size.value else None
+        status = lib.pe_varlen_attn_fwd(ctypes.byref(args), workspace.data_ptr() if workspace is not None else None,
+                                        size.value, stream)
+        _lib.check(status, "pe_varlen_attn_fwd")
+        return out
+    key = _plan_key(args, cu_seqlens)
+    entry = plans.get(key)
+    if entry is None:
+        size = ctypes.c_size_t(0)
+        _lib.check(lib.pe_attn_workspace_size(ctypes.byref(args), ctypes.byref(size)), "pe_attn_workspace_size")
+        workspace = torch.empty(size.value, dtype=torch.uint8, device=q.device) if size.value else None
+        ptr = workspace.data_ptr() if workspace is not None else None
+        _lib.check(lib.pe_attn_plan(ctypes.byref(args), ptr, size.value, stream), "pe_attn_plan")
+        entry = plans[key] = (cu_seqlens, workspace, size.value)
+    _, workspace, nbytes = entry
+    ptr = workspace.data_ptr() if workspace is not None else None
+    _lib.check(lib.pe_attn_short_fwd(ctypes.byref(args), stream), "pe_attn_short_fwd")
+    _lib.check(lib.pe_attn_tiled_fwd(ctypes.byref(args), ptr, nbytes, stream), "pe_attn_tiled_fwd")
     return out
 
 
@@ -231,6 +272,7 @@ def allowed_pairs(n: int, window: tuple[int, int] = (-1, -1), causal: bool = Fal
 
 
 __all__ = [
+    "shared_plans",
     "packed_short_attention",
     "packed_short_attention_supported",
     "select_packed_short_attention_config",

@@ -1,0 +1,182 @@
+"""The packed ModernBERT path on the GPU: pack(), the packed forward, shared tile plans, the
+bucketed HIP-graph runner and the varlen probe, against Hugging Face's own forward.
+
+Oracles: the model's original forward in fp32 (what the reference validates against,
+validate.py:129-170, tests/test_varlen.py:146-434 with random-init weights instead of a
+download), the dense SDPA path of this package, and eager execution for graph replays
+(tests/test_engine.py:29-73). A spy on the C ABI proves the HIP kernels ran (no silent
+fallback) and counts the plan launches the shared-plan scope saves.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def make_model(layers=4, hidden=128, heads=2, local_attention=16, seed=0):
+    from transformers import ModernBertConfig, ModernBertModel
+
+    torch.manual_seed(seed)
+    cfg = ModernBertConfig(vocab_size=1024, hidden_size=hidden, intermediate_size=192, num_hidden_layers=layers,
+                           num_attention_heads=heads, local_attention=local_attention, global_attn_every_n_layers=3,
+                           pad_token_id=0, attn_implementation="sdpa")
+    return ModernBertModel(cfg).eval()
+
+
+def batch(lengths, vocab=1024, seed=1, device="cuda"):
+    g = torch.Generator().manual_seed(seed)
+    S = max(lengths)
+    ids = torch.randint(1, vocab, (len(lengths), S), generator=g)
+    mask = torch.zeros_like(ids)
+    for i, n in enumerate(lengths):
+        mask[i, :n] = 1
+    return ids.to(device), mask.to(device)
+
+
+def token_cosine(a, b):
+    return torch.nn.functional.cosine_similarity(a.float(), b.float(), dim=-1)
+
+
+class Spy:
+    """Counts C-ABI calls made through the loaded library (wraps the ctypes functions)."""
+
+    def __init__(self, monkeypatch):
+        from packed_encoders_amd import _lib
+
+        real = _lib.library()
+        self.calls = {}
+        spy = self
+
+        class Proxy:
+            def __getattr__(self, name):
+                fn = getattr(real, name)
+                if not name.startswith("pe_"):
+                    return fn
+
+                def wrapped(*args):
+                    spy.calls[name] = spy.calls.get(name, 0) + 1
+                    return fn(*args)
+
+                return wrapped
+
+        monkeypatch.setattr(_lib, "library", lambda path=None: Proxy())
+
+
+def test_pack_hip_validates_and_matches_hf_fp32(pe, monkeypatch):
+    announce("pack hip vs HF fp32")
+    ref = make_model().cuda()
+    model = copy.deepcopy(ref).to(torch.bfloat16)
+    ids, mask = batch([300, 37, 129, 5, 64])
+    with torch.no_grad():
+        want = ref(input_ids=ids, attention_mask=mask).last_hidden_state
+    pe.pack(model, attention_backend="hip", validate=True)
+    report = model._packed_encoders.validation_report
+    assert min(report.cosine_by_seq_len.values()) >= 0.98
+    assert report.pieces["attention_bshd"].skipped_reason is None
+    assert report.pieces["attention_bshd"].max_abs_error <= 2e-2
+    spy = Spy(monkeypatch)
+    with torch.no_grad():
+        got = model(input_ids=ids, attention_mask=mask).last_hidden_state
+    live = mask.bool()
+    cos = token_cosine(got[live], want[live])
+    assert cos.min() >= 0.995, cos.min()
+    assert cos.mean() >= 0.999, cos.mean()
+    # 4 layers = 2 global + 2 local: one plan per window kind, a short and a tiled launch per layer
+    assert spy.calls.get("pe_attn_plan") == 2
+    assert spy.calls.get("pe_attn_tiled_fwd") == 4 and spy.calls.get("pe_attn_short_fwd") == 4
+    pe.unpack(model)
+
+
+def test_packed_forward_hip_matches_dense_fallback(pe):
+    from packed_encoders_amd import forward
+
+    announce("packed_forward hip vs sdpa fallback")
+    model = make_model(layers=3).cuda().to(torch.bfloat16)
+    params = pe.config.ModernBertParams.from_hf_config(model.config)
+    ids, mask = batch([513, 1, 90, 257, 33], seed=3)
+    flat, _, cu, max_seqlen, positions = forward.unpad(ids, mask)
+    with torch.no_grad():
+        hip = forward.packed_forward(model, params, flat, cu, max_seqlen, positions, backend="hip")
+        dense = forward.packed_sdpa_fallback(model, params, flat, cu, max_seqlen, positions)
+    cos = token_cosine(hip, dense)
+    assert cos.min() >= 0.995 and cos.mean() >= 0.999, (cos.min(), cos.mean())
+
+
+def test_packed_graph_runner_replays_match_eager(pe):
+    announce("packed graph runner")
+    model = make_model().cuda().to(torch.bfloat16)
+    config = pe.GraphConfig(max_batch=8, max_seq=512, pad_to=64, warmup=2)
+    pe.pack(model, attention_backend="hip", cuda_graph=config, validate=False)
+    engine = pe.get_engine(model)
+    from packed_encoders_amd import forward
+
+    batches = []
+    for lengths, seed in (([300, 100, 37], 5), ([37, 300, 90], 6), ([200, 200, 27], 7)):
+        ids, mask = batch(lengths, seed=seed)
+        flat, _, cu, max_seqlen, positions = forward.unpad(ids, mask)
+        batches.append(pe.PackedBatch(flat, cu, max_seqlen, positions))
+    # same (M bucket, N) for all three; max_seqlen differs for the third
+    with torch.no_grad():
+        eager = []
+        with pe.no_cuda_graph(model):
+            for b in batches:
+                eager.append(engine.forward_packed(b))
+        runner = model._packed_encoders.packed_graph_runner
+        first = [None] * len(batches)
+        for rep in range(3):
+            for i, (b, want) in enumerate(zip(batches, eager)):
+                got = engine.forward_packed(b)
+                torch.cuda.synchronize()
+                # the graph runs the dense layers at the bucketed token count (their GEMMs may
+                # round differently); attention rows are computed identically
+                cos = token_cosine(got, want)
+                assert cos.min() >= 0.999, (rep, i, cos.min())
+                if first[i] is None:
+                    first[i] = got
+                else:
+                    assert torch.equal(got, first[i]), f"replay {rep} of batch {i} is not deterministic"
+                _ = torch.randn(1000, device="cuda").sum()  # unrelated eager work between replays
+    assert runner.captures == 2  # (448, 3, 300) shared by the first two batches; (448, 3, 200)
+    pe.unpack(model)
+
+
+def test_select_attention_picks_hip_for_gqa_causal_and_windows(pe):
+    announce("select_attention")
+    for kw in (dict(n_heads=8, n_kv_heads=2, head_dim=256, causal=True),
+               dict(n_heads=12, n_kv_heads=12, head_dim=64, causal=False, window=(64, 64)),
+               dict(n_heads=4, n_kv_heads=1, head_dim=128, causal=False, window=(10, 3))):
+        choice = pe.select_attention(device=torch.device("cuda"), **kw)
+        assert choice.name == "hip", choice.rejected
+        assert choice.max_abs_err < 2e-2
+        if kw["causal"]:
+            assert choice.prefixed_name == "sdpa" and "hip:prefixed" in choice.rejected
+
+
+def test_modernbert_base_shape_packed_forward(pe):
+    """The C2 model shape (22 layers, hidden 768, 12 x 64, local 128) on a few documents."""
+    from transformers import ModernBertConfig, ModernBertModel
+    from packed_encoders_amd import forward
+
+    announce("ModernBERT-base shape")
+    torch.manual_seed(0)
+    cfg = ModernBertConfig(vocab_size=50368, hidden_size=768, intermediate_size=1152, num_hidden_layers=22,
+                           num_attention_heads=12, local_attention=128, global_attn_every_n_layers=3,
+                           attn_implementation="sdpa")
+    model = ModernBertModel(cfg).eval().cuda().to(torch.bfloat16)
+    params = pe.config.ModernBertParams.from_hf_config(cfg)
+    assert params.head_dim == 64 and params.sliding_half_window == 64
+    ids, mask = batch([400, 1200, 35, 700, 64, 2048], vocab=50368, seed=9)
+    flat, _, cu, max_seqlen, positions = forward.unpad(ids, mask)
+    with torch.no_grad():
+        hip = forward.packed_forward(model, params, flat, cu, max_seqlen, positions, backend="hip")
+        dense = forward.packed_sdpa_fallback(model, params, flat, cu, max_seqlen, positions)
+    cos = token_cosine(hip, dense)
+    assert torch.isfinite(hip).all()
+    assert cos.min() >= 0.99 and cos.mean() >= 0.999, (cos.min(), cos.mean())
