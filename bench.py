@@ -61,13 +61,13 @@ class LayerCall:
     cu_seqlens, the window and the head geometry, so a packed forward builds it once per kind
     (twice for ModernBERT: global and +-64) and every layer of that kind reuses it."""
 
-    def __init__(self, lib, hip, workload, layer, cu, q, k, v, gate, short_max, plans):
+    def __init__(self, lib, hip, workload, layer, cu, q, k, v, gate, short_max, plans, strip=0):
         import torch
 
         self.lib, self.layer = lib, layer
         self.out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
         self.args = hip._args(q, k, v, self.out, cu, workload.max_seqlen, workload.scale, layer.window[0],
-                              layer.window[1], layer.causal, gate, short_max)
+                              layer.window[1], layer.causal, gate, short_max, strip)
         size = ctypes.c_size_t()
         rc = lib.pe_attn_workspace_size(ctypes.byref(self.args), ctypes.byref(size))
         assert rc == 0, rc
@@ -116,8 +116,9 @@ def kernel_instance(stage, workload, layer, short_max):
         return f"pe::short_attn_kernel<{d}, {sk}, {hpw}, {str(layer.gate).lower()}>"
     g = math.gcd(workload.n_heads_q // workload.n_heads_kv, 4)
     bn = 32 if d >= 256 else 64
+    ns = 3 if d == 64 else 2
     win = layer.window != (-1, -1) or layer.causal
-    return f"pe::tiled_attn_kernel<{d}, {g}, {bn}, {str(layer.gate).lower()}, {str(win).lower()}>"
+    return f"pe::tiled_attn_kernel<{d}, {g}, {bn}, {ns}, {str(layer.gate).lower()}, {str(win).lower()}>"
 
 
 def gpu_bench(args, workload):
@@ -142,7 +143,7 @@ def gpu_bench(args, workload):
         k = torch.randn(T, hkv, d, device=dev, generator=gen, dtype=torch.bfloat16)
         v = torch.randn(T, hkv, d, device=dev, generator=gen, dtype=torch.bfloat16)
         g = torch.randn(T, hq, d, device=dev, generator=gen, dtype=torch.bfloat16) if layer.gate else None
-        calls.append(LayerCall(lib, hip, workload, layer, cu, q, k, v, g, short_max, plans))
+        calls.append(LayerCall(lib, hip, workload, layer, cu, q, k, v, g, short_max, plans, args.strip))
     stage, bound, timed_layers = dominant(workload, short_max)
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
@@ -340,6 +341,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="C2", help="C1 C2 C3 C4 C4-band C5 Q4096 (default C2)")
     ap.add_argument("--short-max", type=int, default=None, help="routing boundary (default: gfx950 policy)")
+    ap.add_argument("--strip", type=int, default=0, help="query tiles per tiled-kernel workgroup (0: library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 1 GiB buffer --steps times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define PE_ATTN_ABI_VERSION 1
+#define PE_ATTN_ABI_VERSION 2
 
 #define PE_ATTN_OK 0
 #define PE_ATTN_EINVAL (-1)       /* malformed arguments (maps to ValueError) */
@@ -74,6 +74,10 @@ typedef struct pe_attn_args {
        -1 asks for the library's gfx950 default. At most 128; head_dim 256 always runs the
        tiled kernel (the short kernel covers head_dim <= 128). */
     int32_t short_max;
+    /* Query tiles (of 128 rows; 32 * 4 / gcd(GQA ratio, 4) rows with grouped heads) one
+       workgroup of the tiled kernel walks in sequence, its key/value pipeline running across
+       tile boundaries. 0 asks for the library's default; at most 64. */
+    int32_t strip;
 } pe_attn_args;
 
 /* ABI version of the loaded library; callers compare it with PE_ATTN_ABI_VERSION. */

@@ -12,7 +12,7 @@ from pathlib import Path
 
 from ._build import LIBRARY
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_BF16 = 1
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH = 0, -1, -2, -3, -4
@@ -63,6 +63,7 @@ class AttnArgs(ctypes.Structure):
         ("window_right", ctypes.c_int32),
         ("causal", ctypes.c_int32),
         ("short_max", ctypes.c_int32),
+        ("strip", ctypes.c_int32),
     ]
 
 

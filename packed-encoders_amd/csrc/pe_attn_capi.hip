@@ -20,6 +20,7 @@ namespace {
 using pe::AttnParams;
 
 constexpr int kDefaultShortMax = 64;  // gfx950 default routing boundary (head_dim <= 128)
+constexpr int kMaxStrip = 64;         // query tiles per tiled-kernel workgroup, at most
 
 int gcd_int(int a, int b) {
     while (b) {
@@ -44,6 +45,7 @@ int check_args(const pe_attn_args *a, bool need_pointers = true) {
     if (a->window_left < -1 || a->window_right < -1) return PE_ATTN_EINVAL;
     if (a->causal != 0 && a->causal != 1) return PE_ATTN_EINVAL;
     if (a->short_max < -1 || a->short_max > 128) return PE_ATTN_EINVAL;
+    if (a->strip < 0 || a->strip > kMaxStrip) return PE_ATTN_EINVAL;
     if (!need_pointers || a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
     if (!a->q || !a->k || !a->v || !a->o || !a->cu_seqlens) return PE_ATTN_EINVAL;
     const void *ptrs[4] = {a->q, a->k, a->v, a->o};
@@ -78,14 +80,23 @@ int effective_short_max(const pe_attn_args *a) {
 
 int heads_per_tile(const pe_attn_args *a) { return gcd_int(a->n_heads_q / a->n_heads_kv, 4); }
 
-// Upper bound on (segment, tile) entries the plan can emit, from host-known sizes only.
-int64_t tile_capacity(const pe_attn_args *a, int short_max, int bm) {
+// Upper bound on (segment, strip) entries the plan can emit, from host-known sizes only:
+// a segment of L > short_max tokens has ceil(L / bm) query tiles in ceil(tiles / strip) strips.
+int64_t tile_capacity(const pe_attn_args *a, int short_max, int bm, int strip) {
     if (a->n_seq == 0 || a->total_tokens == 0 || a->max_seqlen <= short_max) return 0;
     const int64_t n = a->n_seq, t = a->total_tokens;
     const int64_t n_long = short_max > 0 ? (t / (short_max + 1) < n ? t / (short_max + 1) : n) : n;
-    const int64_t by_shape = n * ((a->max_seqlen + bm - 1) / bm);
-    const int64_t by_tokens = (t + n_long * (bm - 1)) / bm;
+    const int64_t tiles_per_seg = (a->max_seqlen + bm - 1) / bm;
+    const int64_t by_shape = n * ((tiles_per_seg + strip - 1) / strip);
+    const int64_t tiles_by_tokens = (t + n_long * (bm - 1)) / bm;
+    const int64_t by_tokens = (tiles_by_tokens + n_long * (strip - 1)) / strip;
     return by_shape < by_tokens ? by_shape : by_tokens;
+}
+
+// Query tiles per tiled-kernel workgroup: the caller's choice, else the gfx950 default.
+int effective_strip(const pe_attn_args *a) {
+    if (a->strip > 0) return a->strip;
+    return 1;
 }
 
 AttnParams make_params(const pe_attn_args *a, int short_max) {
@@ -114,6 +125,7 @@ AttnParams make_params(const pe_attn_args *a, int short_max) {
     p.wr = a->window_right;
     if (a->causal) p.wr = 0;  // causal = no key to the right of the query
     p.short_max = short_max;
+    p.strip = effective_strip(a);
     p.c = a->softmax_scale * pe::kLog2e;
     return p;
 }
@@ -156,14 +168,24 @@ int launch_short(const AttnParams &p, int d, bool gate, int short_max, hipStream
     return PE_ATTN_EUNSUPPORTED;
 }
 
+// Key tile and LDS ring depth per head dim: 48 KB (head_dim 64: three workgroups per CU, two
+// tiles in flight each) or 64 KB (head_dim 128 and 256, whose register budget allows at most
+// two and one workgroups per CU).
+template <int D>
+struct TiledShape {
+    static constexpr int BN = D >= 256 ? 32 : 64;
+    static constexpr int NS = D == 64 ? 3 : 2;
+};
+
 template <int D, int G, bool GATE, bool WIN>
 int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
-    constexpr int BN = D >= 256 ? 32 : 64;
+    constexpr int BN = TiledShape<D>::BN, NS = TiledShape<D>::NS;
     p.hgroups = p.hq / G;
     const int64_t blocks = cap * p.hgroups;
     if (blocks <= 0) return PE_ATTN_OK;
     if (blocks > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
-    hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, NS, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                       p);
     return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
 }
 
@@ -192,7 +214,7 @@ constexpr size_t kWorkspaceHeader = 256;  // the entry count lives here, list fo
 
 // Workspace layout: [0, 256) header (int32 entry count), then the (segment, tile) list.
 struct Plan {
-    int sm, g, bm;
+    int sm, g, bm, strip;
     int64_t cap;
 };
 
@@ -202,7 +224,8 @@ int prepare(const pe_attn_args *a, Plan *plan) {
     plan->sm = effective_short_max(a);
     plan->g = heads_per_tile(a);
     plan->bm = 32 * (4 / plan->g);
-    plan->cap = tile_capacity(a, plan->sm, plan->bm);
+    plan->strip = effective_strip(a);
+    plan->cap = tile_capacity(a, plan->sm, plan->bm, plan->strip);
     if (plan->cap > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
     return PE_ATTN_OK;
 }
@@ -237,7 +260,7 @@ int pe_attn_workspace_size(const pe_attn_args *a, size_t *bytes) {
     if (rc) return rc;
     const int sm = effective_short_max(a);
     const int g = heads_per_tile(a);
-    const int64_t cap = tile_capacity(a, sm, 32 * (4 / g));
+    const int64_t cap = tile_capacity(a, sm, 32 * (4 / g), effective_strip(a));
     *bytes = cap > 0 ? kWorkspaceHeader + (size_t)cap * sizeof(int2) : 0;
     return PE_ATTN_OK;
 }
@@ -253,7 +276,7 @@ int pe_attn_plan(const pe_attn_args *a, void *workspace, size_t workspace_bytes,
     int2 *work = reinterpret_cast<int2 *>(static_cast<char *>(workspace) + kWorkspaceHeader);
     const int wr = a->causal ? 0 : a->window_right;
     hipLaunchKernelGGL(pe::plan_kernel, dim3(1), dim3(1024), 0, stream, a->cu_seqlens, a->n_seq, plan.sm, plan.bm,
-                       a->window_left, wr, work, count, (int)plan.cap);
+                       plan.strip, a->window_left, wr, work, count, (int)plan.cap);
     return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
 }
 

@@ -41,6 +41,7 @@ struct AttnParams {
     int32_t wl, wr;  // window (-1: unbounded); causal already folded into wr = 0
     int32_t short_max;
     int32_t hgroups; // head groups per work entry (tiled kernel)
+    int32_t strip;   // query tiles per work entry (tiled kernel)
     float c;         // softmax_scale * log2(e)
     const int2 *work;          // tiled kernel: (segment, q-tile) entries
     const int32_t *work_count; // tiled kernel: number of valid entries

@@ -1,12 +1,13 @@
 // Device-side work planning for the tiled kernel: no host read of cu_seqlens, capture-safe.
 //
 // One 1024-thread workgroup reads cu_seqlens, keeps the segments longer than short_max, splits
-// each into BM-row query tiles and writes (segment, tile) entries ordered by decreasing cost
-// (keys a tile visits: the whole segment, its band, or its causal prefix). Costs are bucketed
-// at half-octave resolution, a counting sort in LDS, so the tiled grid dispatches the
-// longest-running tiles first (longest-processing-time order) and the tail is made of short
-// tiles. Consecutive tiles of a segment with equal cost stay adjacent, so a segment's K/V is
-// read by neighbouring workgroups. Order within a bucket depends on atomics; it changes only
+// each into BM-row query tiles grouped in strips of `strip` consecutive tiles, and writes
+// (segment, first tile) entries ordered by decreasing cost (keys the strip's tiles visit: the
+// whole segment, its band, or its causal prefix, per tile). Costs are bucketed at half-octave
+// resolution, a counting sort in LDS, so the tiled grid dispatches the longest-running strips
+// first (longest-processing-time order) and the tail is made of short strips. Consecutive
+// strips of a segment with equal cost stay adjacent, so a segment's K/V is read by
+// neighbouring workgroups. Order within a bucket depends on atomics; it changes only
 // the schedule, never a result: every output row is produced by exactly one workgroup.
 #pragma once
 
@@ -21,13 +22,21 @@ __device__ __forceinline__ int plan_tile_cost(int t, int bm, int L, int wl, int 
     return max(1, khi - klo);
 }
 
+// Keys visited by the query tiles [s * strip, min(nq, (s + 1) * strip)) of a segment.
+__device__ __forceinline__ int plan_strip_cost(int s, int strip, int nq, int bm, int L, int wl, int wr) {
+    int64_t cost = 0;
+    for (int t = s * strip; t < min(nq, (s + 1) * strip); ++t) cost += plan_tile_cost(t, bm, L, wl, wr);
+    return (int)min(cost, (int64_t)0x7fffffff);
+}
+
 __device__ __forceinline__ int plan_bucket(int cost) {
     const int lg = 31 - __clz(cost);
     const int half = lg >= 1 ? (cost >> (lg - 1)) & 1 : 0;
     return min(63, 2 * lg + half);
 }
 
-__global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, int n_seq, int short_max, int bm,
+// One entry per strip of `strip` consecutive query tiles of `bm` rows: (segment, first tile).
+__global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, int n_seq, int short_max, int bm, int strip,
                                                     int wl, int wr, int2 *work, int32_t *count, int cap) {
     __shared__ int cnt[64];
     __shared__ int off[64];
@@ -37,8 +46,9 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, int n_seq
     for (int seg = tid; seg < n_seq; seg += blockDim.x) {
         const int L = cu[seg + 1] - cu[seg];
         if (L <= short_max) continue;
-        const int nt = (L + bm - 1) / bm;
-        for (int t = 0; t < nt; ++t) atomicAdd(&cnt[plan_bucket(plan_tile_cost(t, bm, L, wl, wr))], 1);
+        const int nq = (L + bm - 1) / bm;
+        const int ns = (nq + strip - 1) / strip;
+        for (int s = 0; s < ns; ++s) atomicAdd(&cnt[plan_bucket(plan_strip_cost(s, strip, nq, bm, L, wl, wr))], 1);
     }
     __syncthreads();
     if (tid == 0) {
@@ -53,17 +63,18 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, int n_seq
     for (int seg = tid; seg < n_seq; seg += blockDim.x) {
         const int L = cu[seg + 1] - cu[seg];
         if (L <= short_max) continue;
-        const int nt = (L + bm - 1) / bm;
-        int t = 0;
-        while (t < nt) {
-            // A run of consecutive tiles in one cost bucket gets one contiguous reservation.
-            const int b = plan_bucket(plan_tile_cost(t, bm, L, wl, wr));
-            int e = t + 1;
-            while (e < nt && plan_bucket(plan_tile_cost(e, bm, L, wl, wr)) == b) ++e;
-            const int pos = atomicAdd(&off[b], e - t);
-            for (int i = 0; i < e - t; ++i)
-                if (pos + i < cap) work[pos + i] = make_int2(seg, t + i);
-            t = e;
+        const int nq = (L + bm - 1) / bm;
+        const int ns = (nq + strip - 1) / strip;
+        int s = 0;
+        while (s < ns) {
+            // A run of consecutive strips in one cost bucket gets one contiguous reservation.
+            const int b = plan_bucket(plan_strip_cost(s, strip, nq, bm, L, wl, wr));
+            int e = s + 1;
+            while (e < ns && plan_bucket(plan_strip_cost(e, strip, nq, bm, L, wl, wr)) == b) ++e;
+            const int pos = atomicAdd(&off[b], e - s);
+            for (int i = 0; i < e - s; ++i)
+                if (pos + i < cap) work[pos + i] = make_int2(seg, (s + i) * strip);
+            s = e;
         }
     }
 }

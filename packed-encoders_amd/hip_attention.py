@@ -37,7 +37,7 @@ def _aligned(t: Tensor) -> Tensor:
 
 def _args(q: Tensor, k: Tensor, v: Tensor, o: Tensor, cu: Tensor, max_seqlen: int, scale: float,
           window_left: int, window_right: int, causal: bool, gate: Tensor | None,
-          short_max: int) -> _lib.AttnArgs:
+          short_max: int, strip: int = 0) -> _lib.AttnArgs:
     a = _lib.AttnArgs()
     a.struct_size = ctypes.sizeof(_lib.AttnArgs)
     a.dtype = _lib.DTYPE_BF16
@@ -58,6 +58,7 @@ def _args(q: Tensor, k: Tensor, v: Tensor, o: Tensor, cu: Tensor, max_seqlen: in
     a.window_left, a.window_right = int(window_left), int(window_right)
     a.causal = 1 if causal else 0
     a.short_max = int(short_max)
+    a.strip = int(strip)
     return a
 
 
@@ -101,7 +102,8 @@ def shared_plans():
 
 def _plan_key(args: _lib.AttnArgs, cu: Tensor) -> tuple:
     return (id(cu), cu.data_ptr(), cu.numel(), args.total_tokens, args.max_seqlen, args.n_heads_q,
-            args.n_heads_kv, args.head_dim, args.window_left, args.window_right, args.causal, args.short_max)
+            args.n_heads_kv, args.head_dim, args.window_left, args.window_right, args.causal, args.short_max,
+            args.strip)
 
 
 def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int,

@@ -241,3 +241,34 @@ def test_out_of_envelope_raises_value_error(pe):
             pe.packed_short_attention(q, k, v, cu, 129, half_window=None, softmax_scale=0.125)
         with pytest.raises(ValueError):
             pe.varlen_attention(q.float(), k, v, cu, 32)
+
+
+@pytest.mark.parametrize("window,causal", [((-1, -1), False), ((64, 64), False), ((-1, -1), True), ((5, 130), False)],
+                         ids=["global", "band64", "causal", "asym"])
+def test_strips_are_bit_identical_and_match_oracle(pe, window, causal):
+    """A workgroup walking a strip of query tiles computes every row exactly as a one-tile
+    workgroup does: outputs are bit-identical for every strip length (including strips that
+    cross into a segment's last, partial tile) and match the oracle."""
+    from packed_encoders_amd import _lib
+    from packed_encoders_amd.hip_attention import _args
+
+    lengths = [700, 65, 1500, 129, 5, 1024]
+    announce(f"strips window={window} causal={causal}")
+    q, k, v, cu, _ = _inputs(lengths, hq=4, hkv=2, seed=31)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    lib = _lib.library()
+    outs = {}
+    for strip in (1, 2, 3, 8, 64):
+        out = torch.full(qd.shape, 3.0, dtype=torch.bfloat16, device="cuda")
+        a = _args(qd, kd, vd, out, cud, max(lengths), 0.125, window[0], window[1], causal, None, 64, strip)
+        size = ctypes.c_size_t()
+        assert lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size)) == 0
+        ws = torch.empty(max(size.value, 1), dtype=torch.uint8, device="cuda")
+        assert lib.pe_varlen_attn_fwd(ctypes.byref(a), ws.data_ptr(), size.value,
+                                      torch.cuda.current_stream().cuda_stream) == 0
+        torch.cuda.synchronize()
+        outs[strip] = out
+    for strip, out in outs.items():
+        assert torch.equal(out, outs[1]), f"strip {strip} differs from strip 1"
+    want = _oracle(q, k, v, cu, scale=0.125, window=window, causal=causal)
+    _assert_parity(outs[1], want, cu)

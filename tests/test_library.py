@@ -54,7 +54,7 @@ def test_library_holds_gfx950_code():
 
 
 def test_abi_version_and_status_text(lib):
-    assert lib.pe_attn_abi_version() == 1
+    assert lib.pe_attn_abi_version() == 2
     assert lib.pe_attn_strerror(0) == b"ok"
     assert lib.pe_attn_strerror(-3) == b"workspace missing or too small"
     assert lib.pe_attn_strerror(-99) == b"unknown status"
@@ -96,11 +96,16 @@ def test_workspace_size_is_host_arithmetic(lib):
     rc, size = _ws(lib, _args(n_heads_q=8, n_heads_kv=2, head_dim=256, max_seqlen=512, n_seq=256, total_tokens=71104))
     assert rc == 0
     assert size == 256 + 8 * min(256 * 16, (71104 + 256 * 31) // 32)
+    # strips of 4 query tiles: min(N * ceil(ceil(S/128)/4), (tiles_by_tokens + N_long*3) // 4)
+    rc, size = _ws(lib, _args(strip=4))
+    tiles = (32438 + n_long * 127) // 128
+    assert rc == 0 and size == 256 + 8 * min(64 * 4, (tiles + n_long * 3) // 4)
 
 
 @pytest.mark.parametrize("field,value,status", [
     ("struct_size", 8, -1), ("dtype", 7, -2), ("head_dim", 96, -2), ("n_heads_kv", 5, -1),
     ("softmax_scale", 0.0, -1), ("window_left", -2, -1), ("causal", 2, -1), ("short_max", 129, -1),
+    ("strip", 65, -1), ("strip", -1, -1),
 ])
 def test_bad_arguments_are_rejected_before_any_launch(lib, field, value, status):
     rc, _ = _ws(lib, _args(**{field: value}))
