@@ -14,6 +14,7 @@
 #include "pe_attn_plan.h"
 #include "pe_attn_short.h"
 #include "pe_attn_tiled.h"
+#include "pe_attn_tiled_wide.h"
 
 namespace {
 
@@ -184,8 +185,12 @@ int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
     const int64_t blocks = cap * p.hgroups;
     if (blocks <= 0) return PE_ATTN_OK;
     if (blocks > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
-    hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, NS, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0, stream,
-                       p);
+    if constexpr (D == 64)
+        hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, NS, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0,
+                           stream, p);
+    else
+        hipLaunchKernelGGL((pe::wide_attn_kernel<D, G, BN, NS, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0,
+                           stream, p);
     return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
 }
 

@@ -119,6 +119,15 @@ __device__ __forceinline__ bf16x8 to_bf16x8(const f32x16 &s, int base) {
     return r;
 }
 
+// acc + p[2i] + p[2i + 1] for one bf16 pair of an MFMA operand, summed in fp32 (v_dot2 with
+// ones): the probabilities the P.V product uses, added without a separate conversion.
+__device__ __forceinline__ float sum2(const bf16x8 &p, int i, float acc) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 pair = {p[2 * i], p[2 * i + 1]};
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(pair, ones, acc, false);
+}
+
 // Transpose four 8-dim key rows (a 4-key x 8-dim chunk) into eight 4-key dim rows of V^T.
 // vt points at the chunk's first dim row, already offset to the permuted key position;
 // pitch is the V^T row pitch in elements.

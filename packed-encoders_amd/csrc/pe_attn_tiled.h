@@ -1,4 +1,5 @@
-// Tiled flash-style packed attention for long segments (gfx950 MFMA).
+// Tiled flash-style packed attention for long segments, head_dim 64 (gfx950 MFMA); wider
+// heads use wide_attn_kernel (pe_attn_tiled_wide.h), which shares the staging below.
 //
 // One workgroup = 4 waves = one strip of consecutive query tiles of one segment, for one group
 // of G query heads. A query tile has 32*4/G rows: the G heads share one kv head (G divides the
@@ -17,20 +18,28 @@
 // 16-lane transpose turns four keys x sixteen dims of the row-major V tile into four keys per
 // lane for one dim each — two of them make one A operand of O^T = V^T . P^T.
 //
-// The workgroup walks its strip as one flat sequence of steps, (query tile, key tile) pairs,
-// through the same ring; the next query tile's Q fragments are prefetched during the last
-// step of the current one (head_dim <= 128). Every global access goes through a buffer
-// resource bounded by the segment, so rows past the segment read as zero with no branch.
-// Block decisions are scalar: each wave skips 32-key blocks outside its rows' band (window /
-// causal), and only blocks crossing a segment or band edge are masked.
+// The ring carries one flat sequence of steps: for each query tile of the strip, 64 / BN "Q
+// steps" that bring the tile's query rows into a stage (each wave reads its 32 rows from there
+// into registers), then one step per key tile. Every step loads the same number of 16-byte
+// units per lane, and past the strip's end the loader issues void steps (out-of-range loads:
+// zeros, no memory traffic), so "this step's loads are done" is one constant s_waitcnt vmcnt.
+// No load the compiler can see remains in the loop (only the gate's), so it never inserts a
+// vector-memory wait of its own that would drain the ring. Every global access goes through a
+// buffer resource bounded by the segment, so rows past the segment read as zero with no
+// branch. Block decisions are scalar: a key tile entirely inside every row's window takes a
+// path with no per-block test; otherwise each wave skips 32-key blocks outside its rows' band
+// (window / causal) and masks only blocks crossing a segment or band edge.
 //
-// Softmax: online, fp32, log2 domain. The running maximum is raised lazily — only when a new
-// tile's maximum exceeds it by more than 2^8 on some lane of the wave — so the accumulator
-// rescale (and the exchange of maxima between the two lanes of a query row) is skipped on
-// almost every tile; numerator and denominator always share the stale maximum, so the result
-// is the same up to rounding. Probabilities are rounded to bf16 for the P.V MFMA and summed
-// unrounded in fp32 (the reference's precision strategy,
-// packed_encoders/_kernels/triton_packed_attention.py:122-136).
+// Softmax: online, fp32, log2 domain, with a running maximum m that is only a reference
+// point: numerator and denominator share it, so any m gives the same result as long as
+// nothing overflows. Maxima are computed on a query tile's first key tile (and while some row
+// of the wave has seen no key yet); later tiles skip them, and a block whose probabilities
+// under the stale m sum past 2^64 on some row (scores jumping by more than ~60 in log2 units)
+// is re-scored exactly, raising m and rescaling the accumulators. Probabilities are rounded to
+// bf16 for the P.V MFMA, and the row sums add exactly those bf16 values in fp32 (v_dot2 with
+// ones), so numerator and denominator weigh every key alike; the reference sums the unrounded
+// fp32 values (packed_encoders/_kernels/triton_packed_attention.py:122-136), a difference far
+// inside the bf16 output rounding.
 //
 // Work entries (segment, first query tile of the strip) come from the device-built,
 // cost-ordered list of plan_kernel; the 1-D grid walks entries with the head group fastest,
@@ -43,8 +52,14 @@
 namespace pe {
 
 constexpr float kLazyRescale = 8.0f;  // log2 of the largest unnormalised probability allowed
+// Largest per-row, per-tile probability sum accepted under a stale running maximum (2^64: far
+// from overflowing the bf16 probabilities, the fp32 sums or the fp32 P.V accumulators).
+constexpr float kOverflowGuard = 18446744073709551616.0f;
 
 #define PE_LDS __attribute__((address_space(3)))
+
+// A buffer offset past every resource's range: the load returns zeros and touches no memory.
+constexpr int kVoidOffset = 0x7ffffff0;
 
 // 16-byte unit of a row after the XOR swizzle: rows of CPR units; ds_read_b128 serves 16 lanes
 // (16 keys, one unit column) per pass over 64 banks, which this makes conflict-free.
@@ -81,7 +96,8 @@ __device__ __forceinline__ bf16x4 tr16(const __bf16 *p) {
 // test folds away at compile time, which also gives global and windowed launches distinct
 // kernel names in traces.
 template <int D, int G, int BN, int NS, bool GATE, bool WIN>
-__global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void tiled_attn_kernel(AttnParams p) {
+    static_assert(D == 64 && BN == 64 && NS == 3, "head_dim 64 kernel (wider heads: wide_attn_kernel)");
     static_assert(D % 32 == 0 && BN % 32 == 0 && (4 % G) == 0 && NS >= 2, "tile shape");
     constexpr int WPH = 4 / G;       // waves per query head
     constexpr int BM = 32 * WPH;     // query rows per query tile
@@ -91,9 +107,11 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
     constexpr int CPR = D / 8;       // 16-byte units per K/V row
     constexpr int TILE = BN * D;     // elements of one K (or V) tile
     constexpr int UPW = TILE / 8 / 64 / 4;  // 1 KB wave-loads per tensor per wave and tile
-    constexpr int LPS = 2 * UPW;     // loads per thread per step (K and V)
-    constexpr bool PREFETCH_Q = false;  // next tile's Q fragments loaded one step early (costs a VGPR occupancy step)
+    constexpr int LPS = 2 * UPW;     // loads per lane per step (K and V, or Q)
+    constexpr int QS = 64 / BN;      // Q steps per query tile
+    constexpr int RQ = 32 / QS;      // query rows per wave and Q step
     static_assert(UPW >= 1 && TILE % (8 * 64 * 4) == 0, "tile must split into 1 KB wave loads");
+    static_assert(64 % BN == 0 && RQ * CPR == LPS * 64, "a Q step must load as much as a K/V step");
 
     __shared__ __attribute__((aligned(16))) __bf16 ring[NS][2][TILE];
 
@@ -124,24 +142,21 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
     const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(p.o + (int64_t)start * p.o_st + (int64_t)qh * p.o_sh, rows_bytes(L, p.o_st, D));
     __amdgpu_buffer_rsrc_t g_rs = o_rs;
     if constexpr (GATE) g_rs = make_rsrc(p.g + (int64_t)start * p.g_st + (int64_t)qh * p.g_sh, rows_bytes(L, p.g_st, D));
-    const int k_row = (int)p.k_st * 2, v_row = (int)p.v_st * 2;
+    const int q_row = (int)p.q_st * 2, k_row = (int)p.k_st * 2, v_row = (int)p.v_st * 2;
 
-    // Key range [klo, klo + ntiles * BN) of query tile qt: the union of its rows' windows.
+    // Key range [klo, klo + ntiles * BN) of query tile qt: the union of its rows' windows
+    // (never empty for a tile inside the segment: each row sees at least itself).
     auto key_range = [&](int qt, int &klo, int &ntiles) {
         const int q0 = qt * BM, rows_end = min(L, q0 + BM);
         klo = wl >= 0 ? max(0, q0 - wl) : 0;
         const int khi = wr >= 0 ? min(L, rows_end + wr) : L;
-        ntiles = khi > klo ? (khi - klo + BN - 1) / BN : 0;
-    };
-    // This wave's 32 query rows of query tile qt as B operands (zero beyond the segment).
-    auto load_q = [&](int qt, bf16x8 (&dst)[DC]) {
-        const int qoff = (qt * BM + rb * 32 + col) * (int)p.q_st * 2 + kg * 16;
-#pragma unroll
-        for (int c = 0; c < DC; ++c) dst[c] = buf_ld16(q_rs, qoff + c * 32, 0);
+        ntiles = max(1, (khi - klo + BN - 1) / BN);
     };
 
-    // DMA geometry: wave-load j of this wave fills units [(wave * UPW + j) * 64, +64) of a tile;
-    // unit u holds key u / CPR, global 16-byte column (u % CPR) ^ swz(key).
+    // DMA geometry. K/V: wave-load j of this wave fills units [(wave * UPW + j) * 64, +64) of a
+    // tile; unit u holds key u / CPR, global 16-byte column (u % CPR) ^ swz(key). Q step i: the
+    // wave's own RQ rows (rows 32 rb + RQ i + r of its head) fill its region of the stage,
+    // unit j * 64 + lane holding row r = unit / CPR, column (unit % CPR) ^ swz(r).
     int koff[UPW], voff[UPW];
 #pragma unroll
     for (int j = 0; j < UPW; ++j) {
@@ -151,8 +166,8 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
         voff[j] = key * v_row + ch * 16;
     }
     const uint32_t ring_base = uniform((int)lds_addr(&ring[0][0][0]));
-    constexpr uint32_t kStageBytes = 2 * TILE * 2, kTileBytes = TILE * 2;
-    auto issue = [&](int stage, int kt0) {
+    constexpr uint32_t kStageBytes = 2 * TILE * 2, kTileBytes = TILE * 2, kQWaveBytes = RQ * D * 2;
+    auto issue_kv = [&](int stage, int kt0) {
         const uint32_t kb = ring_base + stage * kStageBytes + wave * UPW * 1024;
         const int kbase = kt0 * k_row, vbase = kt0 * v_row;
 #pragma unroll
@@ -160,13 +175,28 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
 #pragma unroll
         for (int j = 0; j < UPW; ++j) dma16(kb + kTileBytes + j * 1024, voff[j] + vbase, v_rs);
     };
+    // Q offsets are recomputed at each (rare) Q step rather than held in registers: the empty
+    // asm keeps the compiler from hoisting them out of the loop.
+    auto issue_q = [&](int stage, int qt, int i) {
+        const uint32_t qb = ring_base + stage * kStageBytes + wave * kQWaveBytes;
+        const int base = (qt * BM + rb * 32 + i * RQ) * q_row;
+        int ql = lane;
+        asm volatile("" : "+v"(ql));
+#pragma unroll
+        for (int j = 0; j < LPS; ++j) {
+            const int u = j * 64 + ql;
+            const int r = u / CPR, ch = (u % CPR) ^ swz<CPR>(r);
+            dma16(qb + j * 1024, base + r * q_row + ch * 16, q_rs);
+        }
+    };
 
-    // Per-lane LDS read offsets (elements within a tile). K: key 32b + col, unit 2c + kg.
-    // V^T (tr16): in 16-lane group g = lane / 16, source lane i = lane % 16 points at key
-    // 16h + 4 * (g / 2) + i / 4 (+ 8 for the second half of the operand) and dims
-    // 32 db + 16 (g % 2) + 4 (i % 4); the transpose hands lane (m = dim, kg) four keys of its dim.
-    // Both swizzles depend only on bits of the key below 32 that the block / 16-key-half loops
-    // leave fixed, so every address is a per-lane base plus a compile-time offset.
+    // Per-lane LDS read offsets (elements within a tile). K: key 32b + col, unit 2c + kg (the
+    // wave's Q rows use the same pattern: row col of its region). V^T (tr16): in 16-lane group
+    // g = lane / 16, source lane i = lane % 16 points at key 16h + 4 * (g / 2) + i / 4 (+ 8 for
+    // the second half of the operand) and dims 32 db + 16 (g % 2) + 4 (i % 4); the transpose
+    // hands lane (m = dim, kg) four keys of its dim. Both swizzles depend only on bits of the
+    // key below 16 (CPR 16, 32) or 32 (CPR 8) that the block / 16-key-half loops leave fixed,
+    // so every address is a per-lane base plus a compile-time offset.
     int kbase_c[DC];
 #pragma unroll
     for (int c = 0; c < DC; ++c) kbase_c[c] = col * D + ((2 * c + kg) ^ swz<CPR>(col)) * 8;
@@ -182,106 +212,100 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
             vbase[half][db] = key * D + (((dim >> 3) ^ swz<CPR>(key)) * 8) + (dim & 4);
         }
 
-    f32x16 o[DB];
-    float m;
-    float ls[4];
-    auto reset = [&]() {
+    const float c2 = p.c;
+
+    // Loader: the next step to stage, walked NS - 1 steps ahead of the consumer. Past the
+    // strip's last step it stages "void" steps (out-of-range buffer loads: zeros, no memory
+    // traffic) so that every step issues the same number of loads and the wait below is one
+    // constant count.
+    int ld_qt = qt_first, ld_t = -QS, ld_klo, ld_nt;
+    key_range(ld_qt, ld_klo, ld_nt);
+    auto issue_next = [&](int stage) {
+        if (ld_qt < qt_end) {
+            if (ld_t < 0) issue_q(stage, ld_qt, ld_t + QS);
+            else issue_kv(stage, ld_klo + ld_t * BN);
+            if (++ld_t >= ld_nt) {
+                ++ld_qt;
+                ld_t = -QS;
+                if (ld_qt < qt_end) key_range(ld_qt, ld_klo, ld_nt);
+            }
+        } else {
+            const uint32_t kb = ring_base + stage * kStageBytes + wave * UPW * 1024;
+#pragma unroll
+            for (int j = 0; j < LPS; ++j) dma16(kb + (j % UPW) * 1024 + (j / UPW) * kTileBytes, kVoidOffset, k_rs);
+        }
+    };
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) issue_next(st);
+
+    // Consumer. Two loops, so that the O accumulators of a query tile are carried by the inner
+    // (key tile) loop alone: a flat step loop whose Q steps and tile ends also pass O around
+    // makes the register allocator copy all of it on every step.
+    int stage = 0;  // ring stage of the current step
+    // Start of a step: its loads are complete once at most the NS - 2 later steps' loads are in
+    // flight (loads complete in issue order; other outstanding accesses only make the wait
+    // stricter); after the barrier every wave is done with the previous step's stage, which is
+    // refilled with the step NS - 1 ahead.
+    auto begin_step = [&]() {
+        wait_vmcnt<(NS - 2) * LPS>();
+        __syncthreads();
+        issue_next(stage == 0 ? NS - 1 : stage - 1);
+    };
+    auto end_step = [&]() { stage = stage == NS - 1 ? 0 : stage + 1; };
+
+    bf16x8 qf[DC];
+    for (int qt = qt_first; qt < qt_end; ++qt) {
+        int klo, ntiles;
+        key_range(qt, klo, ntiles);
+        const int r0 = qt * BM + rb * 32;
+        const int myrow = r0 + col;
+        const bool wave_active = r0 < L;
+        const int wr1 = min(L, r0 + 32);
+
+        // Q steps: lanes whose row is in step i's part read their fragments; the empty asm
+        // ends the reads' scope before the next barrier frees the stage.
+#pragma unroll
+        for (int i = 0; i < QS; ++i) {
+            begin_step();
+            if (QS == 1 || col / RQ == i) {
+                const __bf16 *qs = &ring[stage][0][0] + wave * RQ * D - i * RQ * D;
+#pragma unroll
+                for (int c = 0; c < DC; ++c) qf[c] = ld_s16(qs + kbase_c[c]);
+#pragma unroll
+                for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[c]));
+            }
+            end_step();
+        }
+
+        f32x16 o[DB];
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int j = 0; j < 16; ++j) o[db][j] = 0.0f;
-        m = kNegInf;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ls[i] = 0.0f;
-    };
-    const float c2 = p.c;
+        float m = kNegInf;
+        float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        bool need_exact = true;  // some row of the wave may still lack a finite running maximum
 
-    // Current query tile.
-    int qt = qt_first, klo, ntiles;
-    key_range(qt, klo, ntiles);
-    int r0 = qt * BM + rb * 32;
-    int myrow = r0 + col;
-    bool wave_active = r0 < L;
-    int wr1 = min(L, r0 + 32);
-    bf16x8 qf[DC], qn[DC];
-    load_q(qt, qf);
-    reset();
-
-    // Step bookkeeping: a step is (query tile, key tile). `adv` moves a cursor one step ahead.
-    struct Cursor {
-        int qt, t, klo, ntiles;
-    };
-    auto adv = [&](Cursor &c) {
-        if (++c.t >= c.ntiles) {
-            ++c.qt;
-            c.t = 0;
-            if (c.qt < qt_end) key_range(c.qt, c.klo, c.ntiles);
-        }
-    };
-    auto valid = [&](const Cursor &c) { return c.qt < qt_end && c.t < c.ntiles; };
-
-    // Prologue: issue the first NS - 1 steps.
-    Cursor ld{qt, 0, klo, ntiles};  // next step to issue
-    int issued = 0;
-#pragma unroll
-    for (int s = 0; s < NS - 1; ++s) {
-        if (valid(ld)) {
-            issue(issued % NS, ld.klo + ld.t * BN);
-            ++issued;
-            adv(ld);
-        }
-    }
-
-    int t = 0, step = 0;
-    bool first = true;
-    while (true) {
-        // This step's loads are complete once at most the later steps' loads are in flight
-        // (loads complete in issue order).
-        const int later = issued - step - 1;
-        if (NS >= 3 && later >= 2) wait_vmcnt<2 * LPS>();
-        else if (later >= 1) wait_vmcnt<LPS>();
-        else wait_vmcnt<0>();
-        __syncthreads();
-        if (first) {
-            // The query fragments were loaded before this step's K/V (or with the previous
-            // step); ending their load scope here keeps the compiler from waiting on the
-            // vector memory counter inside the loop, which would also drain the ring.
-#pragma unroll
-            for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[c]));
-            first = false;
-        }
-        // The next query tile's Q fragments, during this tile's last step and before the
-        // refill below, so the next step's wait covers them.
-        const bool last_of_tile = t + 1 >= ntiles;
-        const bool more = qt + 1 < qt_end;
-        if constexpr (PREFETCH_Q) {
-            if (last_of_tile && more) load_q(qt + 1, qn);
-        }
-        // Refill the stage freed by the previous step (all waves passed the barrier after it).
-        if (valid(ld)) {
-            issue(issued % NS, ld.klo + ld.t * BN);
-            ++issued;
-            adv(ld);
-        }
-
-        const __bf16 *kt = &ring[step % NS][0][0];
-        const __bf16 *vt = &ring[step % NS][1][0];
-        if (wave_active && t < ntiles) {
-            const int kt0 = klo + t * BN;
-            f32x16 s[NB];
-            bool live[NB];
-            float mp[4] = {kNegInf, kNegInf, kNegInf, kNegInf};  // partial maxima (4 chains)
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const int kb0 = kt0 + 32 * b;
-                live[b] = block_live(kb0, L, r0, wr1, wl, wr);
-                if (live[b]) {
+        for (int t = 0; t < ntiles; ++t) {
+            begin_step();
+            const __bf16 *kt = &ring[stage][0][0];
+            const __bf16 *vt = &ring[stage][1][0];
+            if (wave_active) {
+                const int kt0 = klo + t * BN;
+                // Every block of the tile live and unmasked for all of this wave's rows: the
+                // common case, taken without any per-block test.
+                const bool full = (kt0 + BN <= L) && (wl < 0 || (wr1 - 1) - kt0 <= wl) && (wr < 0 || (kt0 + BN - 1) - r0 <= wr);
+                f32x16 s[NB];
+                bool live[NB];
+                // Raw scores S^T = K . Q^T of 32-key block b, -inf outside the rows' windows.
+                auto scores = [&](int b) {
+                    const int kb0 = kt0 + 32 * b;
                     f32x16 acc;
 #pragma unroll
                     for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
 #pragma unroll
                     for (int c = 0; c < DC; ++c) acc = mfma32(ld_s16(kt + 32 * b * D + kbase_c[c]), qf[c], acc);
-                    if (!block_full(kb0, L, r0, wr1, wl, wr)) {
+                    if (!full && !block_full(kb0, L, r0, wr1, wl, wr)) {
 #pragma unroll
                         for (int j = 0; j < 16; ++j) {
                             const int kk = kb0 + acc_key(j, kg);
@@ -290,92 +314,114 @@ __global__ __launch_bounds__(256) void tiled_attn_kernel(AttnParams p) {
                         }
                     }
                     s[b] = acc;
+                };
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) mp[j & 3] = fmaxf(mp[j & 3], acc[j]);
+                for (int b = 0; b < NB; ++b) {
+                    live[b] = full || block_live(kt0 + 32 * b, L, r0, wr1, wl, wr);
+                    if (live[b]) scores(b);
                 }
-            }
-            // Each lane tests its own maximum: the two lanes of a query row share m, so "some
-            // lane exceeds m" is "some row exceeds m"; only a rescale combines the pair.
-            const float mx = fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]));
-            if (wave_any(mx * c2 > m + kLazyRescale)) {
-                const float mnew = fmaxf(m, fmaxf(mx, __shfl_xor(mx, 32)) * c2);
-                const float alpha = mnew == kNegInf ? 1.0f : exp2_fast(m - mnew);
-                m = mnew;
+                // The running maximum m is only a reference point: numerator and denominator
+                // share it, so any m gives the same result as long as nothing overflows. Maxima
+                // are therefore computed only while some row of the wave lacks a finite m (the
+                // first tiles of a query tile), or for a block whose probabilities under the
+                // stale m sum past kOverflowGuard on some row: that block is scored again and m
+                // raised (a rare exact pass). Otherwise a step spends no VALU on maxima.
+                auto raise_max = [&](int b_lo, int b_hi) {
+                    float mp[4] = {kNegInf, kNegInf, kNegInf, kNegInf};  // partial maxima (4 chains)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) ls[i] *= alpha;
+                    for (int b = 0; b < NB; ++b)
+                        if (b >= b_lo && b < b_hi && live[b]) {
 #pragma unroll
-                for (int db = 0; db < DB; ++db)
+                            for (int j = 0; j < 16; ++j) mp[j & 3] = fmaxf(mp[j & 3], s[b][j]);
+                        }
+                    // Each lane tests its own maximum: the two lanes of a query row share m, so
+                    // "some lane exceeds m" is "some row exceeds m"; only a rescale combines the
+                    // pair.
+                    const float mx = fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]));
+                    if (wave_any(mx * c2 > m + kLazyRescale)) {
+                        const float mnew = fmaxf(m, fmaxf(mx, __shfl_xor(mx, 32)) * c2);
+                        const float alpha = mnew == kNegInf ? 1.0f : exp2_fast(m - mnew);
+                        m = mnew;
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) o[db][j] *= alpha;
-            }
-            const float muse = m == kNegInf ? 0.0f : m;
+                        for (int i = 0; i < 4; ++i) ls[i] *= alpha;
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                if (live[b]) {
+                        for (int db = 0; db < DB; ++db)
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) {
-                        const float e = exp2_fast(fmaf(s[b][j], c2, -muse));
-                        s[b][j] = e;
-                        ls[j & 3] += e;
+                            for (int j = 0; j < 16; ++j) o[db][j] *= alpha;
                     }
+                };
+                // Probabilities of block b under m: bf16 MFMA operands and their fp32 row sums.
+                auto probs = [&](int b, bf16x8 (&pb)[2], float (&st)[4]) {
+                    const float muse = m == kNegInf ? 0.0f : m;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) s[b][j] = exp2_fast(fmaf(s[b][j], c2, -muse));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) st[i] = 0.0f;
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
-                        const bf16x8 pb = to_bf16x8(s[b], 8 * h);
+                        pb[h] = to_bf16x8(s[b], 8 * h);
 #pragma unroll
-                        for (int db = 0; db < DB; ++db) {
-                            // keys 32b + 16h + 8 half + vkey0: the swizzle sees only the bits of
-                            // 8 half + vkey0 (32b + 16h changes neither)
-                            const bf16x4 lo = tr16(vt + (32 * b + 16 * h) * D + vbase[0][db]);
-                            const bf16x4 hi = tr16(vt + (32 * b + 16 * h) * D + vbase[1][db]);
-                            const bf16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                            o[db] = mfma32(va, pb, o[db]);
+                        for (int i = 0; i < 4; ++i) st[i] = sum2(pb[h], i, st[i]);
+                    }
+                };
+                const bool exact = need_exact;
+                if (exact) {
+                    raise_max(0, NB);
+                    need_exact = wave_any((m == kNegInf) & (myrow < L));
+                }
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    if (live[b]) {
+                        bf16x8 pb[2];
+                        float st[4];
+                        probs(b, pb, st);
+                        if (!exact && wave_any(fmaxf(fmaxf(st[0], st[1]), fmaxf(st[2], st[3])) > kOverflowGuard)) {
+                            scores(b);
+                            raise_max(b, b + 1);
+                            probs(b, pb, st);
+                        }
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) ls[i] += st[i];
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                            for (int db = 0; db < DB; ++db) {
+                                // keys 32b + 16h + 8 half + vkey0: the swizzle sees only the bits
+                                // of 8 half + vkey0 (32b + 16h changes neither)
+                                const bf16x4 lo = tr16(vt + (32 * b + 16 * h) * D + vbase[0][db]);
+                                const bf16x4 hi = tr16(vt + (32 * b + 16 * h) * D + vbase[1][db]);
+                                const bf16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                                o[db] = mfma32(va, pb[h], o[db]);
+                            }
                         }
                     }
                 }
             }
+            end_step();
         }
 
-        if (last_of_tile) {
-            // Last key tile of this query tile: normalise, apply the gate, store, reset.
-            const float lsum = (ls[0] + ls[1]) + (ls[2] + ls[3]);
-            const float lt = lsum + __shfl_xor(lsum, 32);
-            if (wave_active) {
-                const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-                const int ooff = myrow * (int)p.o_st * 2;
-                const int goff = GATE ? myrow * (int)p.g_st * 2 : 0;
+        // Normalise, apply the gate, store.
+        const float lsum = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        const float lt = lsum + __shfl_xor(lsum, 32);
+        if (wave_active) {
+            const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+            const int ooff = myrow * (int)p.o_st * 2;
+            const int goff = GATE ? myrow * (int)p.g_st * 2 : 0;
 #pragma unroll
-                for (int db = 0; db < DB; ++db)
+            for (int db = 0; db < DB; ++db)
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const int d0 = db * 32 + 8 * jj + 4 * kg;
-                        bf16x4 g4 = {};
-                        if constexpr (GATE) g4 = buf_ld8(g_rs, goff + d0 * 2, 0);
-                        buf_st8(o_rs, ooff + d0 * 2,
-                                out4<GATE>(o[db][4 * jj] * inv, o[db][4 * jj + 1] * inv, o[db][4 * jj + 2] * inv,
-                                           o[db][4 * jj + 3] * inv, g4));
-                    }
-            }
-            reset();
-            if (!more) break;
-            ++qt;
-            key_range(qt, klo, ntiles);
-            r0 = qt * BM + rb * 32;
-            myrow = r0 + col;
-            wave_active = r0 < L;
-            wr1 = min(L, r0 + 32);
-            if constexpr (PREFETCH_Q) {
-#pragma unroll
-                for (int c = 0; c < DC; ++c) qf[c] = qn[c];
-            } else {
-                load_q(qt, qf);
-            }
-            first = true;  // end the new fragments' load scope after the next barrier
-            t = 0;
-        } else {
-            ++t;
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int d0 = db * 32 + 8 * jj + 4 * kg;
+                    bf16x4 g4 = {};
+                    if constexpr (GATE) g4 = buf_ld8(g_rs, goff + d0 * 2, 0);
+                    buf_st8(o_rs, ooff + d0 * 2,
+                            out4<GATE>(o[db][4 * jj] * inv, o[db][4 * jj + 1] * inv, o[db][4 * jj + 2] * inv,
+                                       o[db][4 * jj + 3] * inv, g4));
+                }
         }
-        ++step;
     }
+    // Loads of void steps may still be landing in LDS: drain before the workgroup ends.
+    wait_vmcnt<0>();
 }
 
 }  // namespace pe

@@ -272,3 +272,28 @@ def test_strips_are_bit_identical_and_match_oracle(pe, window, causal):
         assert torch.equal(out, outs[1]), f"strip {strip} differs from strip 1"
     want = _oracle(q, k, v, cu, scale=0.125, window=window, causal=causal)
     _assert_parity(outs[1], want, cu)
+
+
+@pytest.mark.parametrize("jump", [4.0, 10.0], ids=["below-guard", "past-guard"])
+@pytest.mark.parametrize("window,causal", [((-1, -1), False), ((64, 64), False), ((-1, -1), True)],
+                         ids=["global", "band64", "causal"])
+def test_scores_jumping_past_a_stale_maximum(pe, jump, window, causal):
+    """Keys far into a segment whose scores exceed every earlier score by ~9 * jump (log2
+    units): the tiled kernel's running maximum, taken on a query tile's first key tile, is
+    then far too small. Below the overflow guard (jump 4: probabilities up to ~2^37) the
+    stale maximum is kept; past it (jump 10: ~2^92) the block is re-scored exactly. Both must
+    match the oracle."""
+    lengths = [700, 300, 129]
+    announce(f"score jump={jump} window={window} causal={causal}")
+    q, k, v, cu, _ = _inputs(lengths, hq=4, seed=41)
+    q = q.float().abs().bfloat16()
+    k = k.float()
+    for a in (0, 700):  # keys 200..263 of the first two segments
+        k[a + 200:a + 264] = jump
+    k = k.bfloat16()
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    with torch.inference_mode():
+        got = pe.varlen_attention(qd, kd, vd, cud, max(lengths), softmax_scale=0.125, window=window,
+                                  causal=causal, short_max=0)
+    want = _oracle(q, k, v, cu, scale=0.125, window=window, causal=causal)
+    _assert_parity(got, want, cu)
