@@ -143,6 +143,32 @@ __device__ __forceinline__ void store_vt_chunk(__bf16 *vt, int pitch, const bf16
     }
 }
 
+// Bits lo..hi (clamped to 0..31) of a 32-bit mask; 0 when the range is empty. lo >= 0.
+__device__ __forceinline__ uint32_t bit_range(int lo, int hi) {
+    hi = min(hi, 31);
+    const uint32_t upto = hi >= 31 ? 0xffffffffu : (1u << (max(hi, -1) + 1)) - 1u;
+    const uint32_t below = lo >= 32 ? 0xffffffffu : (1u << lo) - 1u;
+    return hi < lo ? 0u : upto & ~below;
+}
+
+// Per-lane mask of the keys of 32-key block kb0 that row `row` may read, bit x standing for key
+// kb0 + 4 kg + x (the keys of accumulator elements x = acc_key(j, 0) of lane group kg): keys
+// below L and inside the window [row - wl, row + wr] (a negative bound is unbounded).
+__device__ __forceinline__ uint32_t key_mask(int kb0, int kg, int row, int L, int wl, int wr) {
+    const int base = kb0 + 4 * kg;
+    int lo = 0, hi = L - 1 - base;
+    if (wl >= 0) lo = max(lo, row - wl - base);
+    if (wr >= 0) hi = min(hi, row + wr - base);
+    return bit_range(lo, hi);
+}
+
+// Score a, or -inf where bit x of mask m is clear (two VALU: a signed bitfield extract and a
+// bitwise select).
+__device__ __forceinline__ float mask_score(float a, uint32_t m, int x) {
+    const int keep = (int)(m << (31 - x)) >> 31;
+    return __builtin_bit_cast(float, (__builtin_bit_cast(int, a) & keep) | (~keep & (int)0xff800000));
+}
+
 // Whether key block [kb0, kb0 + 32) intersects the keys any row in [r0, r1) may read.
 __device__ __forceinline__ bool block_live(int kb0, int L, int r0, int r1, int wl, int wr) {
     if (kb0 >= L) return false;

@@ -306,12 +306,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
 #pragma unroll
                     for (int c = 0; c < DC; ++c) acc = mfma32(ld_s16(kt + 32 * b * D + kbase_c[c]), qf[c], acc);
                     if (!full && !block_full(kb0, L, r0, wr1, wl, wr)) {
+                        const uint32_t km = key_mask(kb0, kg, myrow, L, wl, wr);
 #pragma unroll
-                        for (int j = 0; j < 16; ++j) {
-                            const int kk = kb0 + acc_key(j, kg);
-                            const bool ok = (kk < L) & ((wl < 0) | (myrow - kk <= wl)) & ((wr < 0) | (kk - myrow <= wr));
-                            acc[j] = ok ? acc[j] : kNegInf;
-                        }
+                        for (int j = 0; j < 16; ++j) acc[j] = mask_score(acc[j], km, acc_key(j, 0));
                     }
                     s[b] = acc;
                 };
