@@ -68,12 +68,23 @@ __device__ __forceinline__ int swz(int key) {
     return CPR == 8 ? (key >> 1) & 7 : key & 15;
 }
 
-// Global -> LDS, 16 bytes per lane: lane l's data lands at lds_base + 16 * l.
-__device__ __forceinline__ void dma16(uint32_t lds_base, int voffset, __amdgpu_buffer_rsrc_t rsrc) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds_base), "v"(voffset), "s"(rsrc)
-                 : "memory", "m0");
+// Global -> LDS, 16 bytes per lane, four loads: load i's lane l data lands at lds[i] + 16 * l;
+// loads 0 and 1 read through rsrc a, loads 2 and 3 through b. M0 (the LDS base register) is
+// saved and restored inside the statement, so the compiler's view of it never changes.
+__device__ __forceinline__ void dma16x4(const uint32_t (&lds)[4], const int (&voff)[4], __amdgpu_buffer_rsrc_t a,
+                                        __amdgpu_buffer_rsrc_t b) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %5, %9, 0 offen lds\n\t"
+        "s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %6, %9, 0 offen lds\n\t"
+        "s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %7, %10, 0 offen lds\n\t"
+        "s_mov_b32 m0, %4\n\tbuffer_load_dwordx4 %8, %10, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(lds[0]), "s"(lds[1]), "s"(lds[2]), "s"(lds[3]), "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]),
+          "s"(a), "s"(b)
+        : "memory");
 }
 
 template <int N>
@@ -167,13 +178,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
     }
     const uint32_t ring_base = uniform((int)lds_addr(&ring[0][0][0]));
     constexpr uint32_t kStageBytes = 2 * TILE * 2, kTileBytes = TILE * 2, kQWaveBytes = RQ * D * 2;
+    static_assert(LPS % 4 == 0 && UPW % 2 == 0, "loads go out four at a time");
+    // LPS loads of one step (lds[i], voff[i]); the first UPW read through ra, the rest rb.
+    auto dma_step = [&](const uint32_t (&lds)[LPS], const int (&off)[LPS], __amdgpu_buffer_rsrc_t ra,
+                        __amdgpu_buffer_rsrc_t rb) {
+#pragma unroll
+        for (int g = 0; g < LPS / 4; ++g) {
+            const uint32_t l4[4] = {lds[4 * g], lds[4 * g + 1], lds[4 * g + 2], lds[4 * g + 3]};
+            const int o4[4] = {off[4 * g], off[4 * g + 1], off[4 * g + 2], off[4 * g + 3]};
+            dma16x4(l4, o4, 4 * g < UPW ? ra : rb, 4 * g + 2 < UPW ? ra : rb);
+        }
+    };
     auto issue_kv = [&](int stage, int kt0) {
         const uint32_t kb = ring_base + stage * kStageBytes + wave * UPW * 1024;
         const int kbase = kt0 * k_row, vbase = kt0 * v_row;
+        uint32_t lds[LPS];
+        int off[LPS];
 #pragma unroll
-        for (int j = 0; j < UPW; ++j) dma16(kb + j * 1024, koff[j] + kbase, k_rs);
-#pragma unroll
-        for (int j = 0; j < UPW; ++j) dma16(kb + kTileBytes + j * 1024, voff[j] + vbase, v_rs);
+        for (int j = 0; j < UPW; ++j) {
+            lds[j] = kb + j * 1024;
+            off[j] = koff[j] + kbase;
+            lds[UPW + j] = kb + kTileBytes + j * 1024;
+            off[UPW + j] = voff[j] + vbase;
+        }
+        dma_step(lds, off, k_rs, v_rs);
     };
     // Q offsets are recomputed at each (rare) Q step rather than held in registers: the empty
     // asm keeps the compiler from hoisting them out of the loop.
@@ -182,12 +210,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
         const int base = (qt * BM + rb * 32 + i * RQ) * q_row;
         int ql = lane;
         asm volatile("" : "+v"(ql));
+        uint32_t lds[LPS];
+        int off[LPS];
 #pragma unroll
         for (int j = 0; j < LPS; ++j) {
             const int u = j * 64 + ql;
             const int r = u / CPR, ch = (u % CPR) ^ swz<CPR>(r);
-            dma16(qb + j * 1024, base + r * q_row + ch * 16, q_rs);
+            lds[j] = qb + j * 1024;
+            off[j] = base + r * q_row + ch * 16;
         }
+        dma_step(lds, off, q_rs, q_rs);
     };
 
     // Per-lane LDS read offsets (elements within a tile). K: key 32b + col, unit 2c + kg (the
@@ -231,8 +263,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
             }
         } else {
             const uint32_t kb = ring_base + stage * kStageBytes + wave * UPW * 1024;
+            uint32_t lds[LPS];
+            int off[LPS];
 #pragma unroll
-            for (int j = 0; j < LPS; ++j) dma16(kb + (j % UPW) * 1024 + (j / UPW) * kTileBytes, kVoidOffset, k_rs);
+            for (int j = 0; j < LPS; ++j) {
+                lds[j] = kb + (j % UPW) * 1024 + (j / UPW) * kTileBytes;
+                off[j] = kVoidOffset;
+            }
+            dma_step(lds, off, k_rs, k_rs);
         }
     };
 #pragma unroll

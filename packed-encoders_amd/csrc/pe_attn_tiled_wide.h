@@ -83,13 +83,30 @@ __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
     }
     const uint32_t ring_base = uniform((int)lds_addr(&ring[0][0][0]));
     constexpr uint32_t kStageBytes = 2 * TILE * 2, kTileBytes = TILE * 2, kQWaveBytes = RQ * D * 2;
+    static_assert(LPS % 4 == 0 && UPW % 2 == 0, "loads go out four at a time");
+    // LPS loads of one step (lds[i], voff[i]); the first UPW read through ra, the rest rb.
+    auto dma_step = [&](const uint32_t (&lds)[LPS], const int (&off)[LPS], __amdgpu_buffer_rsrc_t ra,
+                        __amdgpu_buffer_rsrc_t rb) {
+#pragma unroll
+        for (int g = 0; g < LPS / 4; ++g) {
+            const uint32_t l4[4] = {lds[4 * g], lds[4 * g + 1], lds[4 * g + 2], lds[4 * g + 3]};
+            const int o4[4] = {off[4 * g], off[4 * g + 1], off[4 * g + 2], off[4 * g + 3]};
+            dma16x4(l4, o4, 4 * g < UPW ? ra : rb, 4 * g + 2 < UPW ? ra : rb);
+        }
+    };
     auto issue_kv = [&](int stage, int kt0) {
         const uint32_t kb = ring_base + stage * kStageBytes + wave * UPW * 1024;
         const int kbase = kt0 * k_row, vbase = kt0 * v_row;
+        uint32_t lds[LPS];
+        int off[LPS];
 #pragma unroll
-        for (int j = 0; j < UPW; ++j) dma16(kb + j * 1024, koff[j] + kbase, k_rs);
-#pragma unroll
-        for (int j = 0; j < UPW; ++j) dma16(kb + kTileBytes + j * 1024, voff[j] + vbase, v_rs);
+        for (int j = 0; j < UPW; ++j) {
+            lds[j] = kb + j * 1024;
+            off[j] = koff[j] + kbase;
+            lds[UPW + j] = kb + kTileBytes + j * 1024;
+            off[UPW + j] = voff[j] + vbase;
+        }
+        dma_step(lds, off, k_rs, v_rs);
     };
     // Q offsets are recomputed at each (rare) Q step rather than held in registers: the empty
     // asm keeps the compiler from hoisting them out of the loop.
@@ -98,12 +115,16 @@ __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
         const int base = (qt * BM + rb * 32 + i * RQ) * q_row;
         int ql = lane;
         asm volatile("" : "+v"(ql));
+        uint32_t lds[LPS];
+        int off[LPS];
 #pragma unroll
         for (int j = 0; j < LPS; ++j) {
             const int u = j * 64 + ql;
             const int r = u / CPR, ch = (u % CPR) ^ swz<CPR>(r);
-            dma16(qb + j * 1024, base + r * q_row + ch * 16, q_rs);
+            lds[j] = qb + j * 1024;
+            off[j] = base + r * q_row + ch * 16;
         }
+        dma_step(lds, off, q_rs, q_rs);
     };
 
     // Per-lane LDS read offsets (elements within a tile). K: key 32b + col, unit 2c + kg (the
