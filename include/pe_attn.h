@@ -16,8 +16,9 @@
  *                  && (!causal || j <= i)
  *     out[i] = sum_j softmax_j(scale * q_i . k_j over allowed j) * v_j
  *   Arithmetic: fp32 scores and accumulation; probabilities are rounded to bf16 before the
- *   P.V product and the normaliser is the fp32 sum of the unrounded probabilities; the output
- *   is rounded to bf16. With a gate, out = bf16(bf16(out) * bf16(sigmoid(gate))).
+ *   P.V product and the normaliser is an fp32 sum of the probabilities (of their bf16-rounded
+ *   values in the head_dim-64 tiled kernel, of the unrounded ones elsewhere); the output is
+ *   rounded to bf16. With a gate, out = bf16(bf16(out) * bf16(sigmoid(gate))).
  *   Rows at or beyond cu_seqlens[n_seq] are never written. Empty segments are allowed.
  *   Caller contract (not checked on device): cu_seqlens[0] = 0, non-decreasing,
  *   cu_seqlens[n_seq] <= total_tokens, and max_seqlen >= every segment length.
