@@ -18,7 +18,12 @@ schedule on the host's cores with the reference's own CPU kernel (oracle/_ref) f
 short-global layers and per-segment fp32 torch SDPA for global layers longer than 128 (the
 reference's rule).
 
+For C2 the line also carries ``end_to_end``: the whole packed ModernBERT-base forward
+(random-init weights, bf16) over the same batch through ``pe.pack``, eager and replayed from
+the bucketed HIP-graph runner, in tokens/s.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2] [--no-cpu-baseline]
+                       [--no-model]
 """
 
 from __future__ import annotations
@@ -235,6 +240,68 @@ def sanity_check(calls, workload, cu):
         raise SystemExit(f"bench output check failed: max-abs {err}")
 
 
+def model_bench(args, workload):
+    """End-to-end ModernBERT-base (random init, bf16) over the workload's packed batch: the
+    packed forward through ``pe.pack`` (embeddings, 22 layers with this library's attention,
+    final norm), eager and replayed from the bucketed HIP-graph runner. Returns tokens/s and
+    ms per forward of both, timed with events around K forwards after W warm-ups."""
+    import torch
+    from transformers import ModernBertConfig, ModernBertModel
+
+    import packed_encoders_amd as pe
+    from packed_encoders_amd import forward
+
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    cfg = ModernBertConfig(vocab_size=50368, hidden_size=768, intermediate_size=1152, num_hidden_layers=22,
+                           num_attention_heads=12, local_attention=128, global_attn_every_n_layers=3,
+                           global_rope_theta=160000.0, local_rope_theta=10000.0, attn_implementation="sdpa")
+    model = ModernBertModel(cfg).eval().to(dev, torch.bfloat16)
+    lengths = workload.lengths
+    g = torch.Generator(device=dev).manual_seed(77)
+    ids = torch.randint(0, cfg.vocab_size, (sum(lengths),), device=dev, generator=g)
+    cu = torch.tensor(workload.cu_seqlens(), dtype=torch.int32, device=dev)
+    positions = torch.cat([torch.arange(n, device=dev) for n in lengths])
+    batch = pe.PackedBatch(ids, cu, max(lengths), positions)
+    gcfg = pe.GraphConfig(max_batch=len(lengths), max_seq=max(lengths), pad_to=256, warmup=2)
+    pe.pack(model, attention_backend="hip", cuda_graph=gcfg, validate=False)
+    engine = pe.get_engine(model)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for _ in range(max(args.warmup, 2)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / args.steps
+        return wall, e0.elapsed_time(e1) / args.steps
+
+    res = {"model": "ModernBERT-base, 22 layers, hidden 768, 12x64, GeGLU 1152, vocab 50368, random init, bf16",
+           "tokens": workload.total_tokens}
+    with torch.no_grad():
+        with pe.no_cuda_graph(model):
+            wall, gpu = timed(lambda: engine.forward_packed(batch))
+            eager_out = engine.forward_packed(batch)
+        res["eager_ms"] = round(wall, 3)
+        res["eager_tokens_per_s"] = round(workload.total_tokens / (wall * 1e-3), 1)
+        wall, gpu = timed(lambda: engine.forward_packed(batch))
+        graph_out = engine.forward_packed(batch)
+        res["graph_ms"] = round(wall, 3)
+        res["graph_tokens_per_s"] = round(workload.total_tokens / (wall * 1e-3), 1)
+        cos = torch.nn.functional.cosine_similarity(graph_out.float(), eager_out.float(), dim=-1)
+        res["graph_vs_eager_min_cosine"] = round(float(cos.min()), 5)
+    log(f"model: eager {res['eager_ms']:.2f} ms ({res['eager_tokens_per_s'] / 1e6:.2f} M tokens/s), "
+        f"graph {res['graph_ms']:.2f} ms ({res['graph_tokens_per_s'] / 1e6:.2f} M tokens/s)")
+    pe.unpack(model)
+    return res
+
+
 def traffic_from_profiles(workload_name: str, kernel: str):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if one exists."""
     path = ROOT / "profiles" / "traffic.json"
@@ -344,6 +411,8 @@ def main() -> int:
     ap.add_argument("--short-max", type=int, default=None, help="routing boundary (default: gfx950 policy)")
     ap.add_argument("--strip", type=int, default=0, help="query tiles per tiled-kernel workgroup (0: library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the end-to-end packed ModernBERT forward (C2 only)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 1 GiB buffer --steps times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -362,6 +431,13 @@ def main() -> int:
                 "C4-band": lambda: pe.workloads.c4(band=True), "C5": pe.workloads.c5,
                 "Q4096": pe.workloads.query_sweep}[w]()
     res = gpu_bench(args, workload)
+    model_res = None
+    if w == "C2" and not args.no_model:
+        try:
+            model_res = model_bench(args, workload)
+        except Exception as exc:  # reported, never required
+            model_res = {"error": f"{type(exc).__name__}: {exc}"}
+            log(f"model leg skipped: {model_res['error']}")
     cpu_res = None
     if not args.no_cpu_baseline:
         calls, cu = res.pop("_outputs")
@@ -402,6 +478,8 @@ def main() -> int:
         "roofline": res["roofline"],
         "cpu_baseline": cpu_res,
     }
+    if model_res is not None:
+        line["end_to_end"] = model_res
     print(json.dumps(line), flush=True)
     return 0
 

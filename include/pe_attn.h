@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define PE_ATTN_ABI_VERSION 2
+#define PE_ATTN_ABI_VERSION 3
 
 #define PE_ATTN_OK 0
 #define PE_ATTN_EINVAL (-1)       /* malformed arguments (maps to ValueError) */
@@ -126,6 +126,35 @@ int pe_packed_short_attn_fwd(const pe_attn_args *args, hipStream_t stream);
    Replaces select_packed_short_attention_config
    (packed_encoders/_kernels/triton_packed_attention.py:29-42). */
 int pe_attn_short_config(int32_t max_seqlen, int32_t head_dim, int32_t out[4]);
+
+/* Split-half rotary embedding straight from the packed QKV projection: the producer of the
+   layout the attention entry points read (q, k contiguous [n_rows, n_heads, head_dim]; v stays
+   a strided view of qkv). Row r of qkv [n_rows, 3 * n_heads * head_dim] (q at column 0, k at
+   n_heads * head_dim) uses row r % table_rows of the cos / sin tables [table_rows, head_dim]:
+   per-token gathered tables for a packed batch, [S, head_dim] tables for a dense [B, S] one.
+     q_out[r, h, i]       = bf16(q[i] * cos[i] - q[i + D/2] * sin[i])
+     q_out[r, h, i + D/2] = bf16(q[i + D/2] * cos[i + D/2] + q[i] * sin[i + D/2])   (i < D/2)
+   in fp32 with each product rounded before the sum; k likewise. 16-byte alignment of every
+   row is required (pointers % 16 == 0, strides % 8 == 0). */
+typedef struct pe_rope_args {
+    uint32_t struct_size; /* sizeof(pe_rope_args) */
+    int32_t dtype;        /* PE_ATTN_DTYPE_BF16 */
+    const void *qkv;      /* [n_rows, 3 * n_heads * head_dim], row stride qkv_stride_row */
+    const void *cos;      /* [table_rows, head_dim], row stride table_stride_row */
+    const void *sin;      /* same shape and stride as cos */
+    void *q_out;          /* [n_rows, n_heads, head_dim] contiguous (written) */
+    void *k_out;          /* [n_rows, n_heads, head_dim] contiguous (written) */
+    int64_t qkv_stride_row;   /* elements */
+    int64_t table_stride_row; /* elements */
+    int32_t table_rows;
+    int32_t n_rows;
+    int32_t n_heads;
+    int32_t head_dim; /* 64, 128 or 256 */
+} pe_rope_args;
+
+/* Replaces apply_rope_bshd (packed_encoders/_kernels/rope.py:302-349) on the packed attention
+   path (packed_encoders/ops.py:464-499). */
+int pe_rope_qkv_fwd(const pe_rope_args *args, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,7 @@ from pathlib import Path
 
 from ._build import LIBRARY
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 DTYPE_BF16 = 1
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH = 0, -1, -2, -3, -4
@@ -27,6 +27,7 @@ EXPORTED = (
     "pe_attn_tiled_fwd",
     "pe_packed_short_attn_fwd",
     "pe_attn_short_config",
+    "pe_rope_qkv_fwd",
 )
 
 
@@ -67,6 +68,26 @@ class AttnArgs(ctypes.Structure):
     ]
 
 
+class RopeArgs(ctypes.Structure):
+    """Mirror of ``pe_rope_args``."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("dtype", ctypes.c_int32),
+        ("qkv", ctypes.c_void_p),
+        ("cos", ctypes.c_void_p),
+        ("sin", ctypes.c_void_p),
+        ("q_out", ctypes.c_void_p),
+        ("k_out", ctypes.c_void_p),
+        ("qkv_stride_row", ctypes.c_int64),
+        ("table_stride_row", ctypes.c_int64),
+        ("table_rows", ctypes.c_int32),
+        ("n_rows", ctypes.c_int32),
+        ("n_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+    ]
+
+
 @lru_cache(maxsize=1)
 def library(path: str | None = None) -> ctypes.CDLL:
     """Load the in-tree library once; ``ImportError`` if it is missing or mismatched."""
@@ -97,6 +118,8 @@ def library(path: str | None = None) -> ctypes.CDLL:
     lib.pe_packed_short_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p]
     lib.pe_attn_short_config.restype = ctypes.c_int
     lib.pe_attn_short_config.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32)]
+    lib.pe_rope_qkv_fwd.restype = ctypes.c_int
+    lib.pe_rope_qkv_fwd.argtypes = [ctypes.POINTER(RopeArgs), ctypes.c_void_p]
     version = lib.pe_attn_abi_version()
     if version != ABI_VERSION:
         raise ImportError(f"{lib_path} has ABI {version}, expected {ABI_VERSION}: rebuild it")

@@ -1,5 +1,5 @@
 // C ABI of libpe_attn.so (declared in include/pe_attn.h): argument checks, host-side sizing
-// and the launches of the plan, short and tiled kernels on the caller's stream.
+// and the launches of the plan, short, tiled and RoPE kernels on the caller's stream.
 //
 // Nothing here reads device memory, synchronises or allocates, so every entry point can be
 // captured into a HIP graph. No exception crosses the ABI; failures are status codes.
@@ -15,6 +15,7 @@
 #include "pe_attn_short.h"
 #include "pe_attn_tiled.h"
 #include "pe_attn_tiled_wide.h"
+#include "pe_rope.h"
 
 namespace {
 
@@ -242,6 +243,15 @@ int check_workspace(const Plan &plan, const void *workspace, size_t bytes) {
     return PE_ATTN_OK;
 }
 
+template <int D>
+int launch_rope(const pe::RopeParams &p, hipStream_t stream) {
+    const int64_t threads = (int64_t)p.n_rows * 2 * p.heads * (D / 16);
+    const int64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
+    hipLaunchKernelGGL(pe::rope_qkv_kernel<D>, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
+}
+
 }  // namespace
 
 extern "C" {
@@ -339,6 +349,35 @@ int pe_attn_short_config(int32_t max_seqlen, int32_t head_dim, int32_t out[4]) {
     out[2] = hpw;
     out[3] = 4;
     return PE_ATTN_OK;
+}
+
+int pe_rope_qkv_fwd(const pe_rope_args *a, hipStream_t stream) {
+    if (!a || a->struct_size != sizeof(pe_rope_args)) return PE_ATTN_EINVAL;
+    if (a->dtype != PE_ATTN_DTYPE_BF16) return PE_ATTN_EUNSUPPORTED;
+    if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return PE_ATTN_EUNSUPPORTED;
+    if (a->n_rows < 0 || a->n_heads < 1 || a->table_rows < 1) return PE_ATTN_EINVAL;
+    if (a->n_rows == 0) return PE_ATTN_OK;
+    if (!a->qkv || !a->cos || !a->sin || !a->q_out || !a->k_out) return PE_ATTN_EINVAL;
+    const void *ptrs[5] = {a->qkv, a->cos, a->sin, a->q_out, a->k_out};
+    for (const void *p : ptrs)
+        if (!aligned16(p)) return PE_ATTN_EINVAL;
+    const int64_t width = 3LL * a->n_heads * a->head_dim;
+    if (a->qkv_stride_row < width || (a->qkv_stride_row & 7)) return PE_ATTN_EINVAL;
+    if (a->table_stride_row < a->head_dim || (a->table_stride_row & 7)) return PE_ATTN_EINVAL;
+    pe::RopeParams p;
+    p.qkv = static_cast<const __bf16 *>(a->qkv);
+    p.cos = static_cast<const __bf16 *>(a->cos);
+    p.sin = static_cast<const __bf16 *>(a->sin);
+    p.q_out = static_cast<__bf16 *>(a->q_out);
+    p.k_out = static_cast<__bf16 *>(a->k_out);
+    p.qkv_st = a->qkv_stride_row;
+    p.table_st = a->table_stride_row;
+    p.table_rows = a->table_rows;
+    p.n_rows = a->n_rows;
+    p.heads = a->n_heads;
+    if (a->head_dim == 64) return launch_rope<64>(p, stream);
+    if (a->head_dim == 128) return launch_rope<128>(p, stream);
+    return launch_rope<256>(p, stream);
 }
 
 }  // extern "C"

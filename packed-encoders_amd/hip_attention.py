@@ -8,8 +8,10 @@ names, argument meaning and error behaviour (``ValueError`` outside the envelope
 gate) that replaces the reference's FlashAttention varlen calls.
 
 All compute goes through ``libpe_attn.so`` (include/pe_attn.h) on the current HIP stream via
-the ``pe_hip::varlen_attention`` / ``pe_hip::packed_short_attention`` torch ops. There is no
-CPU or eager-PyTorch fallback: if the library is missing, the loader raises ``ImportError``.
+the ``pe_hip::varlen_attention`` / ``pe_hip::packed_short_attention`` torch ops, and the
+producer of their q/k layout, ``rope_qkv`` (``pe_hip::rope_qkv``: RoPE straight from the packed
+QKV projection). There is no CPU or eager-PyTorch fallback: if the library is missing, the
+loader raises ``ImportError``.
 """
 
 from __future__ import annotations
@@ -163,6 +165,46 @@ def _meta(q: Tensor, *args, **kwargs) -> Tensor:
     return torch.empty(q.shape, dtype=_BF16, device=q.device)
 
 
+def _rope_tables(cos: Tensor, sin: Tensor, d: int) -> tuple[Tensor, Tensor]:
+    if cos.ndim == 3:  # [1, rows, D] or per-row [B, S, D]
+        cos, sin = cos.reshape(-1, d), sin.reshape(-1, d)
+    if cos.ndim != 2 or cos.shape[-1] != d or sin.shape != cos.shape:
+        raise ValueError(f"cos/sin must be [rows, {d}] (or [1, rows, {d}]), got {tuple(cos.shape)}")
+    return cos, sin
+
+
+def _rope_impl(qkv: Tensor, cos: Tensor, sin: Tensor, h: int, d: int) -> list[Tensor]:
+    if qkv.dtype != _BF16 or cos.dtype != _BF16 or sin.dtype != _BF16:
+        raise ValueError("rope_qkv computes in bf16")
+    if qkv.shape[-1] != 3 * h * d:
+        raise ValueError(f"qkv last dim {qkv.shape[-1]} != 3*{h}*{d}")
+    cos, sin = _rope_tables(cos, sin, d)
+    flat = qkv.reshape(-1, 3 * h * d)
+    if flat.stride(-1) != 1 or flat.data_ptr() % 16 or flat.stride(0) % 8:
+        flat = flat.contiguous()
+    cos = cos if (cos.stride(-1) == 1 and cos.data_ptr() % 16 == 0 and cos.stride(0) % 8 == 0) else cos.contiguous()
+    sin = sin if (sin.stride(-1) == 1 and sin.data_ptr() % 16 == 0 and sin.stride(0) % 8 == 0) else sin.contiguous()
+    n = flat.shape[0]
+    q = torch.empty(n, h, d, dtype=_BF16, device=qkv.device)
+    k = torch.empty(n, h, d, dtype=_BF16, device=qkv.device)
+    if n:
+        a = _lib.RopeArgs()
+        a.struct_size = ctypes.sizeof(_lib.RopeArgs)
+        a.dtype = _lib.DTYPE_BF16
+        a.qkv, a.cos, a.sin, a.q_out, a.k_out = flat.data_ptr(), cos.data_ptr(), sin.data_ptr(), q.data_ptr(), k.data_ptr()
+        a.qkv_stride_row, a.table_stride_row = flat.stride(0), cos.stride(0)
+        a.table_rows, a.n_rows, a.n_heads, a.head_dim = cos.shape[0], n, h, d
+        stream = torch.cuda.current_stream(qkv.device).cuda_stream
+        _lib.check(_lib.library().pe_rope_qkv_fwd(ctypes.byref(a), stream), "pe_rope_qkv_fwd")
+    shape = tuple(qkv.shape[:-1]) + (h, d)
+    return [q.view(shape), k.view(shape)]
+
+
+def _rope_meta(qkv: Tensor, cos: Tensor, sin: Tensor, h: int, d: int) -> list[Tensor]:
+    shape = tuple(qkv.shape[:-1]) + (h, d)
+    return [torch.empty(shape, dtype=_BF16, device=qkv.device), torch.empty(shape, dtype=_BF16, device=qkv.device)]
+
+
 def _register() -> None:
     """Define ``pe_hip::varlen_attention`` and ``pe_hip::packed_short_attention`` once per process."""
     lib = torch.library.Library("pe_hip", "FRAGMENT")
@@ -172,12 +214,15 @@ def _register() -> None:
                    "int short_max) -> Tensor")
         lib.define("packed_short_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, int max_seqlen, "
                    "float softmax_scale, int window_left, int window_right) -> Tensor")
+        lib.define("rope_qkv(Tensor qkv, Tensor cos, Tensor sin, int h, int d) -> Tensor[]")
     except RuntimeError:
         return  # already defined by an earlier import in this process
     lib.impl("varlen_attention", _varlen_impl, "CUDA")
     lib.impl("varlen_attention", _meta, "Meta")
     lib.impl("packed_short_attention", _short_impl, "CUDA")
     lib.impl("packed_short_attention", _meta, "Meta")
+    lib.impl("rope_qkv", _rope_impl, "CUDA")
+    lib.impl("rope_qkv", _rope_meta, "Meta")
     globals()["_TORCH_LIBRARY"] = lib
 
 
@@ -282,3 +327,18 @@ __all__ = [
     "useful_flops",
     "allowed_pairs",
 ]
+
+
+def rope_qkv(qkv: Tensor, h: int, d: int, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor]:
+    """Split-half RoPE'd q, k read straight from the packed projection ``qkv [..., 3*h*d]``
+    (bf16, on the GPU), returned contiguous ``[..., h, d]`` — the layout ``varlen_attention``
+    reads, with v left as a strided view of ``qkv``. ``cos``/``sin`` are ``[rows, d]`` (or
+    ``[B or 1, S, d]``, flattened to rows): row ``r`` of ``qkv`` (leading dims flattened) uses
+    table row ``r % rows``, so per-token gathered tables (rows = tokens) and dense ``[S, d]``
+    tables of a ``[B, S]`` batch both work. Same contract as the reference's ``apply_rope_bshd``
+    (packed_encoders/_kernels/rope.py:302-349); ``ValueError`` for bad shapes or dtypes."""
+    if not qkv.is_cuda:
+        raise ValueError("rope_qkv runs on the HIP device")
+    q, k = torch.ops.pe_hip.rope_qkv(qkv, cos, sin, int(h), int(d))
+    return q, k
+

@@ -73,7 +73,14 @@ def rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor
 def rope_qkv(qkv: Tensor, h: int, d: int, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor]:
     """RoPE read straight from the packed projection ``qkv [B, S, 3*h*d]``: returns contiguous
     ``[B, S, h, d]`` q and k, the layout the varlen kernels read. ``cos``/``sin`` are
-    ``[B or 1, S, d]`` (for packed input: the tables gathered by each token's position)."""
+    ``[B or 1, S, d]`` (for packed input: the tables gathered by each token's position).
+    On the GPU in bf16 this is the HIP kernel (``hip_attention.rope_qkv``, the reference's
+    apply_rope_bshd, _kernels/rope.py:302-349); fp32 inputs (the pieces' oracles) and CPU
+    tensors take the same formula in torch."""
+    if qkv.is_cuda and qkv.dtype == torch.bfloat16:
+        from .hip_attention import rope_qkv as hip_rope_qkv
+
+        return hip_rope_qkv(qkv, h, d, cos, sin)
     view = qkv.view(*qkv.shape[:-1], 3, h, d)
     c, s = cos[..., None, :], sin[..., None, :]
     return _rotate(view[..., 0, :, :], c, s).contiguous(), _rotate(view[..., 1, :, :], c, s).contiguous()

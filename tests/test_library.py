@@ -54,7 +54,7 @@ def test_library_holds_gfx950_code():
 
 
 def test_abi_version_and_status_text(lib):
-    assert lib.pe_attn_abi_version() == 2
+    assert lib.pe_attn_abi_version() == 3
     assert lib.pe_attn_strerror(0) == b"ok"
     assert lib.pe_attn_strerror(-3) == b"workspace missing or too small"
     assert lib.pe_attn_strerror(-99) == b"unknown status"
@@ -140,3 +140,37 @@ def test_short_config_table(lib):
 def test_python_config_mirror(pe):
     cfg = pe.select_packed_short_attention_config(100)
     assert cfg == {"block_m": 32, "key_capacity": 128, "heads_per_workgroup": 2, "num_waves": 4}
+
+
+def _rope_args(**kw):
+    from packed_encoders_amd import _lib
+
+    a = _lib.RopeArgs()
+    a.struct_size = ctypes.sizeof(_lib.RopeArgs)
+    a.dtype = 1
+    a.qkv_stride_row, a.table_stride_row = 3 * 12 * 64, 64
+    a.table_rows, a.n_rows, a.n_heads, a.head_dim = 128, 128, 12, 64
+    for name, value in kw.items():
+        setattr(a, name, value)
+    return a
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("struct_size", 8, -1), ("dtype", 2, -2), ("head_dim", 96, -2), ("n_heads", 0, -1), ("table_rows", 0, -1),
+    ("n_rows", -1, -1),
+])
+def test_rope_bad_arguments_are_rejected_before_any_launch(lib, field, value, status):
+    assert lib.pe_rope_qkv_fwd(ctypes.byref(_rope_args(**{field: value})), None) == status
+
+
+def test_rope_missing_pointers_misaligned_strides_and_empty_input(lib):
+    assert lib.pe_rope_qkv_fwd(ctypes.byref(_rope_args()), None) == -1  # NULL pointers, rows to do
+    assert lib.pe_rope_qkv_fwd(ctypes.byref(_rope_args(n_rows=0)), None) == 0  # nothing to do
+    buf = ctypes.create_string_buffer(64)
+    p = (ctypes.addressof(buf) + 15) & ~15
+    a = _rope_args(qkv=p, cos=p, sin=p, q_out=p, k_out=p, qkv_stride_row=3 * 12 * 64 + 4)
+    assert lib.pe_rope_qkv_fwd(ctypes.byref(a), None) == -1  # row stride not a multiple of 8
+    a = _rope_args(qkv=p, cos=p, sin=p, q_out=p, k_out=p, qkv_stride_row=3 * 12 * 64 - 8)
+    assert lib.pe_rope_qkv_fwd(ctypes.byref(a), None) == -1  # rows narrower than 3HD
+    a = _rope_args(qkv=p + 2, cos=p, sin=p, q_out=p, k_out=p)
+    assert lib.pe_rope_qkv_fwd(ctypes.byref(a), None) == -1  # misaligned base
