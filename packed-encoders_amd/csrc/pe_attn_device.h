@@ -91,22 +91,7 @@ __device__ __forceinline__ bf16x8 ld_g16(const __bf16 *p) {
 __device__ __forceinline__ bf16x8 ld_s16(const __bf16 *p) {
     return *reinterpret_cast<const bf16x8 *>(p);
 }
-__device__ __forceinline__ void st_s16(__bf16 *p, bf16x8 x) { *reinterpret_cast<bf16x8 *>(p) = x; }
-__device__ __forceinline__ void st_s8(__bf16 *p, bf16x4 x) { *reinterpret_cast<bf16x4 *>(p) = x; }
-
-__device__ __forceinline__ bf16x8 zero8() {
-    bf16x8 z;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) z[i] = (__bf16)0.0f;
-    return z;
-}
-
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Position of key k inside a 32-key block of the transposed V tile (bits 2 and 3 swapped).
-__device__ __forceinline__ int vperm(int k) {
-    return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
-}
 
 // Key index (within its 32-key block) of accumulator element j held by lane group kg.
 __device__ __forceinline__ int acc_key(int j, int kg) { return 8 * (j >> 2) + 4 * kg + (j & 3); }
@@ -126,21 +111,6 @@ __device__ __forceinline__ float sum2(const bf16x8 &p, int i, float acc) {
     const bf16x2 pair = {p[2 * i], p[2 * i + 1]};
     const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
     return __builtin_amdgcn_fdot2_f32_bf16(pair, ones, acc, false);
-}
-
-// Transpose four 8-dim key rows (a 4-key x 8-dim chunk) into eight 4-key dim rows of V^T.
-// vt points at the chunk's first dim row, already offset to the permuted key position;
-// pitch is the V^T row pitch in elements.
-__device__ __forceinline__ void store_vt_chunk(__bf16 *vt, int pitch, const bf16x8 (&rows)[4]) {
-#pragma unroll
-    for (int dd = 0; dd < 8; ++dd) {
-        bf16x4 t;
-        t[0] = rows[0][dd];
-        t[1] = rows[1][dd];
-        t[2] = rows[2][dd];
-        t[3] = rows[3][dd];
-        st_s8(vt + dd * pitch, t);
-    }
 }
 
 // Bits lo..hi (clamped to 0..31) of a 32-bit mask; 0 when the range is empty. lo >= 0.
@@ -203,29 +173,6 @@ __device__ __forceinline__ bf16x4 out4(float a0, float a1, float a2, float a3, b
         }
     }
     return r;
-}
-
-// Store 4 consecutive output dims of one row, with the optional fused sigmoid gate:
-// y = bf16(bf16(o) * bf16(sigmoid(g))) (the rounding order of the reference's gate kernel,
-// packed_encoders/_kernels/hybrid.py:197-206).
-template <bool GATE>
-__device__ __forceinline__ void store_out4(__bf16 *orow, const __bf16 *grow, float a0, float a1,
-                                           float a2, float a3) {
-    bf16x4 r;
-    r[0] = (__bf16)a0;
-    r[1] = (__bf16)a1;
-    r[2] = (__bf16)a2;
-    r[3] = (__bf16)a3;
-    if constexpr (GATE) {
-        bf16x4 g = *reinterpret_cast<const bf16x4 *>(grow);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float gs = 1.0f / (1.0f + __expf(-(float)g[i]));
-            float sg = (float)(__bf16)gs;
-            r[i] = (__bf16)((float)r[i] * sg);
-        }
-    }
-    *reinterpret_cast<bf16x4 *>(orow) = r;
 }
 
 }  // namespace pe

@@ -1,11 +1,15 @@
 // LDS-resident packed attention for short segments (length <= SK <= 128), gfx950 MFMA.
 //
-// One workgroup = 4 waves = one segment x HPW query heads. The segment's whole K (row-major)
-// and V (transposed) tiles of every head in the group are staged in LDS once; Q rows go
-// straight to registers as MFMA B operands. Each wave owns one head and walks that head's
-// 32-row query blocks (4 / HPW waves share a head). A query block sees every key of the
-// segment at once, so the softmax is exact, with no online rescaling: the row maximum and sum
-// are per-lane scalars combined with the partner lane through one wavefront shuffle.
+// One workgroup = 4 waves = one segment x HPW query heads. The segment's whole K and V tiles
+// of every head in the group are staged in LDS once, row-major with the 16-byte units of a row
+// XOR-swizzled (swz), by direct global-to-LDS loads; the wave's query blocks go straight to
+// registers as MFMA B operands. Every load of the workgroup — query blocks first, then all K/V
+// tiles — is issued before the one wait, so a workgroup pays the memory latency once. Each
+// wave owns one head and walks that head's 32-row query blocks (4 / HPW waves share a head).
+// S^T = K.Q^T reads K with ds_read_b128 and O^T = V^T.P^T reads V^T with ds_read_b64_tr_b16,
+// as the tiled kernels do. A query block sees every key of the segment at once, so the softmax
+// is exact, with no online rescaling: the row maximum and sum are per-lane scalars combined
+// with the partner lane through one wavefront shuffle.
 //
 // Segments longer than short_max, or empty, leave the workgroup at once, which is what lets
 // one launch of this kernel and one of the tiled kernel split a mixed batch per segment with
@@ -13,86 +17,104 @@
 // segment: rows past its end read as zero and are never written.
 #pragma once
 
-#include "pe_attn_device.h"
+#include "pe_attn_stage.h"
 
 namespace pe {
 
 template <int D, int SK, int HPW, bool GATE>
 __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
     static_assert(SK % 32 == 0 && SK <= 128 && (4 % HPW) == 0, "short tile shape");
-    constexpr int KP = D + 8;
-    constexpr int VP = SK + 8;
     constexpr int NB = SK / 32;
     constexpr int DC = D / 16;
     constexpr int DB = D / 32;
-    constexpr int WSTEP = 4 / HPW;  // waves sharing one head
+    constexpr int CPR = D / 8;                    // 16-byte units per row
+    constexpr int WSTEP = 4 / HPW;                // waves sharing one head
+    constexpr int NQ = (NB + WSTEP - 1) / WSTEP;  // query blocks per wave, at most
+    constexpr int TILE = SK * D;                  // elements of one K (or V) tile
+    constexpr int UPT = TILE / 8 / 256;           // 16-byte units per thread and tile
+    static_assert(UPT >= 1 && TILE % (8 * 256) == 0, "a tile must split into 1 KB wave loads");
 
-    __shared__ __attribute__((aligned(16))) __bf16 Ks[HPW][SK * KP];
-    __shared__ __attribute__((aligned(16))) __bf16 Vt[HPW][D * VP];
+    __shared__ __attribute__((aligned(16))) __bf16 kv[HPW][2][TILE];
 
     const int seg = blockIdx.x;
     const int start = p.cu[seg];
     const int L = p.cu[seg + 1] - start;
     if (L <= 0 || L > p.short_max) return;
     const int h0 = blockIdx.y * HPW;
-    const int nkb = (L + 31) >> 5;
-    const int kcap = nkb * 32;
     const int tid = threadIdx.x;
-    const int k_row = (int)p.k_st * 2, v_row = (int)p.v_st * 2;
-
-    // Stage K and V^T of every head of the group (keys >= L read as zero up to the block edge).
-#pragma unroll
-    for (int s = 0; s < HPW; ++s) {
-        const int qh = h0 + s;
-        if (qh >= p.hq) break;
-        const int kvh = qh / p.group;
-        const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(p.k + (int64_t)start * p.k_st + (int64_t)kvh * p.k_sh, rows_bytes(L, p.k_st, D));
-        const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(p.v + (int64_t)start * p.v_st + (int64_t)kvh * p.v_sh, rows_bytes(L, p.v_st, D));
-        for (int c = tid; c < kcap * (D / 8); c += 256) {
-            const int key = c / (D / 8), dc = c - key * (D / 8);
-            st_s16(&Ks[s][key * KP + dc * 8], buf_ld16(k_rs, key * k_row + dc * 16, 0));
-        }
-        // 2-key x 8-dim chunks, key pair fastest across threads.
-        const int npairs = kcap / 2;
-        for (int c = tid; c < npairs * (D / 8); c += 256) {
-            const int kp = c % npairs, dc = c / npairs;
-            const bf16x8 a = buf_ld16(v_rs, 2 * kp * v_row + dc * 16, 0);
-            const bf16x8 b = buf_ld16(v_rs, (2 * kp + 1) * v_row + dc * 16, 0);
-            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-            __bf16 *dst = &Vt[s][(dc * 8) * VP + vperm(2 * kp)];
-#pragma unroll
-            for (int dd = 0; dd < 8; ++dd) {
-                bf16x2 t;
-                t[0] = a[dd];
-                t[1] = b[dd];
-                *reinterpret_cast<bf16x2 *>(dst + dd * VP) = t;
-            }
-        }
-    }
-    __syncthreads();
-
     const int lane = tid & 63;
     const int wave = uniform(tid >> 6);
     const int col = lane & 31, kg = lane >> 5;
     const int s = wave % HPW;
     const int qh = h0 + s;
-    if (qh >= p.hq) return;
+    const bool wave_head = qh < p.hq;
+
+    // The wave's query blocks as B operands (zero beyond the segment), issued first.
+    const __amdgpu_buffer_rsrc_t q_rs = make_rsrc(p.q + (int64_t)start * p.q_st + (int64_t)min(qh, p.hq - 1) * p.q_sh,
+                                                  rows_bytes(L, p.q_st, D));
+    bf16x8 qf[NQ][DC];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int qoff = (32 * (wave / HPW + i * WSTEP) + col) * (int)p.q_st * 2 + kg * 16;
+#pragma unroll
+        for (int c = 0; c < DC; ++c) qf[i][c] = buf_ld16(q_rs, qoff + c * 32, 0);
+    }
+
+    // K and V of every head of the group: unit u = (j * 4 + wave) * 64 + lane of a tile holds
+    // key u / CPR, global column (u % CPR) ^ swz(key); keys >= L read as zero.
+    const int k_row = (int)p.k_st * 2, v_row = (int)p.v_st * 2;
+    const uint32_t kv_base = uniform((int)lds_addr(&kv[0][0][0]));
+#pragma unroll
+    for (int hs = 0; hs < HPW; ++hs) {
+        const int h = h0 + hs;
+        if (h >= p.hq) break;
+        const int kvh = h / p.group;
+        const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(p.k + (int64_t)start * p.k_st + (int64_t)kvh * p.k_sh, rows_bytes(L, p.k_st, D));
+        const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(p.v + (int64_t)start * p.v_st + (int64_t)kvh * p.v_sh, rows_bytes(L, p.v_st, D));
+#pragma unroll
+        for (int j = 0; j < UPT; ++j) {
+            const int u = (j * 4 + wave) * 64 + lane;
+            const int key = u / CPR, ch = (u % CPR) ^ swz<CPR>(key);
+            const uint32_t dst = kv_base + (uint32_t)((hs * 2 * TILE) * 2 + (j * 4 + wave) * 1024);
+            dma16(dst, key * k_row + ch * 16, k_rs);
+            dma16(dst + TILE * 2, key * v_row + ch * 16, v_rs);
+        }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (!wave_head) return;
+
+    // Per-lane LDS offsets: K key 32b + col, unit 2c + kg; V^T as in the tiled kernels.
+    int kbase_c[DC];
+#pragma unroll
+    for (int c = 0; c < DC; ++c) kbase_c[c] = col * D + ((2 * c + kg) ^ swz<CPR>(col)) * 8;
+    const int vi = lane & 15, vg = lane >> 4;
+    const int vkey0 = 4 * (vg >> 1) + (vi >> 2);
+    const int vdim0 = 16 * (vg & 1) + 4 * (vi & 3);
+    int vbase[2][DB];
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const int key = 8 * half + vkey0, dim = 32 * db + vdim0;
+            vbase[half][db] = key * D + (((dim >> 3) ^ swz<CPR>(key)) * 8) + (dim & 4);
+        }
+    const __bf16 *kt = &kv[s][0][0];
+    const __bf16 *vt = &kv[s][1][0];
+
     const int wl = p.wl, wr = p.wr;
     const float c2 = p.c;
-    const __amdgpu_buffer_rsrc_t q_rs = make_rsrc(p.q + (int64_t)start * p.q_st + (int64_t)qh * p.q_sh, rows_bytes(L, p.q_st, D));
+    const int nkb = (L + 31) >> 5;
     const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(p.o + (int64_t)start * p.o_st + (int64_t)qh * p.o_sh, rows_bytes(L, p.o_st, D));
     __amdgpu_buffer_rsrc_t g_rs = o_rs;
     if constexpr (GATE) g_rs = make_rsrc(p.g + (int64_t)start * p.g_st + (int64_t)qh * p.g_sh, rows_bytes(L, p.g_st, D));
 
-    for (int qb = wave / HPW; qb * 32 < L; qb += WSTEP) {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int qb = wave / HPW + i * WSTEP;
+        if (qb * 32 >= L) break;
         const int r0 = qb * 32, r1 = min(L, r0 + 32);
         const int myrow = r0 + col;
-        bf16x8 qf[DC];
-        {
-            const int qoff = myrow * (int)p.q_st * 2 + kg * 16;
-#pragma unroll
-            for (int c = 0; c < DC; ++c) qf[c] = buf_ld16(q_rs, qoff + c * 32, 0);
-        }
         f32x16 sc[NB];
         bool live[NB];
         float mx = kNegInf;
@@ -101,19 +123,15 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
             const int kb0 = 32 * b;
             live[b] = b < nkb && block_live(kb0, L, r0, r1, wl, wr);
             if (live[b]) {
-                const __bf16 *ka = &Ks[s][(kb0 + col) * KP + kg * 8];
                 f32x16 acc;
 #pragma unroll
                 for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
 #pragma unroll
-                for (int c = 0; c < DC; ++c) acc = mfma32(ld_s16(ka + c * 16), qf[c], acc);
+                for (int c = 0; c < DC; ++c) acc = mfma32(ld_s16(kt + kb0 * D + kbase_c[c]), qf[i][c], acc);
                 if (!block_full(kb0, L, r0, r1, wl, wr)) {
+                    const uint32_t km = key_mask(kb0, kg, myrow, L, wl, wr);
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) {
-                        const int key = kb0 + acc_key(j, kg);
-                        const bool ok = (key < L) & ((wl < 0) | (myrow - key <= wl)) & ((wr < 0) | (key - myrow <= wr));
-                        acc[j] = ok ? acc[j] : kNegInf;
-                    }
+                    for (int j = 0; j < 16; ++j) acc[j] = mask_score(acc[j], km, acc_key(j, 0));
                 }
                 sc[b] = acc;
 #pragma unroll
@@ -140,9 +158,13 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const bf16x8 pb = to_bf16x8(sc[b], 8 * h);
-                    const __bf16 *va = &Vt[s][col * VP + 32 * b + 16 * h + 8 * kg];
 #pragma unroll
-                    for (int db = 0; db < DB; ++db) o[db] = mfma32(ld_s16(va + db * 32 * VP), pb, o[db]);
+                    for (int db = 0; db < DB; ++db) {
+                        const bf16x4 lo = tr16(vt + (32 * b + 16 * h) * D + vbase[0][db]);
+                        const bf16x4 hi = tr16(vt + (32 * b + 16 * h) * D + vbase[1][db]);
+                        const bf16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                        o[db] = mfma32(va, pb, o[db]);
+                    }
                 }
             }
         }

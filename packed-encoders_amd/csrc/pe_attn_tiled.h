@@ -47,7 +47,7 @@
 // (longest-processing-time order).
 #pragma once
 
-#include "pe_attn_device.h"
+#include "pe_attn_stage.h"
 
 namespace pe {
 
@@ -55,53 +55,6 @@ constexpr float kLazyRescale = 8.0f;  // log2 of the largest unnormalised probab
 // Largest per-row, per-tile probability sum accepted under a stale running maximum (2^64: far
 // from overflowing the bf16 probabilities, the fp32 sums or the fp32 P.V accumulators).
 constexpr float kOverflowGuard = 18446744073709551616.0f;
-
-#define PE_LDS __attribute__((address_space(3)))
-
-// A buffer offset past every resource's range: the load returns zeros and touches no memory.
-constexpr int kVoidOffset = 0x7ffffff0;
-
-// 16-byte unit of a row after the XOR swizzle: rows of CPR units; ds_read_b128 serves 16 lanes
-// (16 keys, one unit column) per pass over 64 banks, which this makes conflict-free.
-template <int CPR>
-__device__ __forceinline__ int swz(int key) {
-    return CPR == 8 ? (key >> 1) & 7 : key & 15;
-}
-
-// Global -> LDS, 16 bytes per lane, four loads: load i's lane l data lands at lds[i] + 16 * l;
-// loads 0 and 1 read through rsrc a, loads 2 and 3 through b. M0 (the LDS base register) is
-// saved and restored inside the statement, so the compiler's view of it never changes.
-__device__ __forceinline__ void dma16x4(const uint32_t (&lds)[4], const int (&voff)[4], __amdgpu_buffer_rsrc_t a,
-                                        __amdgpu_buffer_rsrc_t b) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %5, %9, 0 offen lds\n\t"
-        "s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %6, %9, 0 offen lds\n\t"
-        "s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %7, %10, 0 offen lds\n\t"
-        "s_mov_b32 m0, %4\n\tbuffer_load_dwordx4 %8, %10, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(lds[0]), "s"(lds[1]), "s"(lds[2]), "s"(lds[3]), "v"(voff[0]), "v"(voff[1]), "v"(voff[2]), "v"(voff[3]),
-          "s"(a), "s"(b)
-        : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const PE_LDS void *)p;
-}
-
-// ds_read_b64_tr_b16 at an LDS element address: in each 16-lane group, lane j receives element
-// j % 4 of the 4-element rows addressed by lanes j / 4, j / 4 + 4, j / 4 + 8 and j / 4 + 12.
-__device__ __forceinline__ bf16x4 tr16(const __bf16 *p) {
-    typedef __bf16 lds_bf16x4 __attribute__((ext_vector_type(4)));
-    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((PE_LDS lds_bf16x4 *)(PE_LDS void *)p);
-}
 
 // WIN: the call has a window or causal bound. Without one (global attention) every window
 // test folds away at compile time, which also gives global and windowed launches distinct
