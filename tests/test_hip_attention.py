@@ -299,45 +299,40 @@ def test_scores_jumping_past_a_stale_maximum(pe, jump, window, causal):
     _assert_parity(got, want, cu)
 
 
-def _torch_rope_qkv(qkv, h, d, cos, sin):
-    """The fp32 formula x * cos + rotate_half(x) * sin, rounded once to bf16 (the CPU path of
-    ops.rope_qkv, run here on CPU tensors)."""
-    from packed_encoders_amd import ops
-
-    q, k = ops.rope_qkv(qkv.cpu(), h, d, cos.cpu(), sin.cpu())
-    return q, k
-
-
 @pytest.mark.parametrize("d,h", [(64, 12), (128, 6), (256, 8), (64, 1)])
 @pytest.mark.parametrize("tables", ["per-token", "dense-modulo", "batched"])
-def test_rope_qkv_is_bit_exact_against_the_fp32_formula(pe, d, h, tables):
-    """pe_rope_qkv_fwd through the torch op: q, k bit-identical to the fp32 formula, v untouched,
-    for per-token gathered tables, dense [S, D] tables reused across a batch (row % S), and
-    per-row [B, S, D] tables; qkv rows wider than 3HD (a strided slice) included."""
-    from packed_encoders_amd import hip_attention, ops
+def test_rope_qkv_is_bit_exact_against_the_oracle(pe, d, h, tables):
+    """pe_rope_qkv_fwd through the torch op: q, k bit-identical to the CPU oracle
+    (oracle/rope.py), v untouched, for per-token gathered tables, dense [S, D] tables reused
+    across a batch (row % S), and per-row [B, S, D] tables; qkv rows wider than 3HD (a
+    strided slice) included."""
+    from oracle import rope
+    from packed_encoders_amd import hip_attention
 
     announce(f"rope_qkv d={d} h={h} tables={tables}")
-    g = torch.Generator().manual_seed(d + h)
+    rng = np.random.default_rng(d + h)
     B, S = 3, 37
-    wide = torch.randn(B, S, 3 * h * d + 64, generator=g).bfloat16()
-    qkv = wide[..., : 3 * h * d]  # row stride 3HD + 64
-    cos_full, sin_full = ops.rope_tables(4096, d, 10000.0, "cpu", torch.bfloat16)
+    wide = oa.to_bf16(rng.standard_normal((B, S, 3 * h * d + 64)))
+    cos_np, sin_np = rope.rope_tables(4096, d, 10000.0)
     if tables == "per-token":
-        pos = torch.randint(0, 4096, (B * S,), generator=g)
-        cos, sin = cos_full[0, pos][None], sin_full[0, pos][None]
-        x = qkv.reshape(1, B * S, -1)
+        pos = rng.integers(0, 4096, B * S)
+        cos, sin = cos_np[pos][None], sin_np[pos][None]
+        shape = (1, B * S)
     elif tables == "dense-modulo":
-        cos, sin = cos_full[:, :S], sin_full[:, :S]
-        x = qkv
+        cos, sin = cos_np[:S][None], sin_np[:S][None]
+        shape = (B, S)
     else:
-        pos = torch.randint(0, 4096, (B, S), generator=g)
-        cos, sin = cos_full[0][pos], sin_full[0][pos]
-        x = qkv
-    want_q, want_k = _torch_rope_qkv(x, h, d, cos, sin)
-    xd = x.cuda()
+        pos = rng.integers(0, 4096, (B, S))
+        cos, sin = cos_np[pos], sin_np[pos]
+        shape = (B, S)
+    rows = B * S
+    want_q, want_k = rope.rope_qkv(wide.reshape(rows, -1), h, d, cos.reshape(-1, d), sin.reshape(-1, d))
+    xd = torch.from_numpy(wide).bfloat16().cuda()[..., : 3 * h * d].reshape(*shape, 3 * h * d)
+    before = xd.clone()
+    cd, sd = torch.from_numpy(cos).bfloat16().cuda(), torch.from_numpy(sin).bfloat16().cuda()
     with torch.inference_mode():
-        got_q, got_k = hip_attention.rope_qkv(xd, h, d, cos.cuda(), sin.cuda())
-    assert got_q.shape == want_q.shape and got_q.is_contiguous() and got_k.is_contiguous()
-    assert torch.equal(got_q.cpu(), want_q)
-    assert torch.equal(got_k.cpu(), want_k)
-    assert torch.equal(xd.cpu(), x)  # qkv (v included) is read only
+        got_q, got_k = hip_attention.rope_qkv(xd, h, d, cd, sd)
+    assert got_q.shape == (*shape, h, d) and got_q.is_contiguous() and got_k.is_contiguous()
+    assert np.array_equal(got_q.float().cpu().numpy().reshape(rows, h, d), want_q)
+    assert np.array_equal(got_k.float().cpu().numpy().reshape(rows, h, d), want_k)
+    assert torch.equal(xd, before)  # qkv (v included) is read only

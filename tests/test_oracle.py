@@ -159,3 +159,65 @@ def test_allowed_pairs_closed_form(pe):
         assert allowed_pairs(L, causal=True) == L * (L + 1) // 2
         mask = oa.allowed_mask(L, L, (w, w))
         assert allowed_pairs(L, (w, w)) == int(mask.sum())
+
+
+def test_rope_oracle_closed_forms():
+    from oracle import rope
+
+    rng = np.random.default_rng(5)
+    d = 64
+    x = oa.to_bf16(rng.standard_normal((7, d)))
+    cos, sin = rope.rope_tables(8, d, 10000.0)
+    # position 0: cos = 1, sin = 0 -> identity
+    assert np.array_equal(rope.rotate(x, cos[0], sin[0]), x)
+    # a quarter turn on every pair: (a, b) -> (-b, a) exactly
+    quarter_c, quarter_s = np.zeros(d, np.float32), np.ones(d, np.float32)
+    turned = rope.rotate(x, quarter_c, quarter_s)
+    assert np.array_equal(turned[:, : d // 2], -x[:, d // 2:])
+    assert np.array_equal(turned[:, d // 2:], x[:, : d // 2])
+    # norms of (x_i, x_{i + d/2}) pairs are kept up to the rounding of the tables and outputs
+    r = rope.rotate(x, cos[5], sin[5])
+    n0 = x[:, : d // 2] ** 2 + x[:, d // 2:] ** 2
+    n1 = r[:, : d // 2] ** 2 + r[:, d // 2:] ** 2
+    assert np.allclose(n1, n0, rtol=2e-2, atol=1e-3)
+
+
+def test_rope_oracle_composes_rotations():
+    from oracle import rope
+
+    rng = np.random.default_rng(6)
+    d = 64
+    x = rng.standard_normal((5, d)).astype(np.float32)
+    inv = 1.0 / (10000.0 ** (np.arange(0, d, 2) / d))
+    def exact(v, pos):  # float64 rotation, no rounding
+        a = np.concatenate([pos * inv, pos * inv])
+        h = d // 2
+        return np.concatenate([v[:, :h] * np.cos(a[:h]) - v[:, h:] * np.sin(a[:h]),
+                               v[:, h:] * np.cos(a[h:]) + v[:, :h] * np.sin(a[h:])], axis=1)
+    # the bf16 pipeline at position p + q stays close to rotating by p, then by q
+    cos, sin = rope.rope_tables(64, d, 10000.0)
+    direct = rope.rotate(oa.to_bf16(x), cos[30], sin[30])
+    assert np.allclose(direct, exact(exact(x, 10), 20), atol=5e-2)
+
+
+def test_rope_oracle_matches_torch_fp32_formula_bit_exactly():
+    import torch
+
+    from oracle import rope
+
+    rng = np.random.default_rng(7)
+    h, d, rows = 3, 64, 11
+    qkv = oa.to_bf16(rng.standard_normal((rows, 3 * h * d)))
+    cos, sin = rope.rope_tables(rows, d, 160000.0)
+    q, k = rope.rope_qkv(qkv, h, d, cos, sin)
+    t = torch.from_numpy(qkv).view(rows, 3, h, d)
+    c = torch.from_numpy(cos)[:, None, :]
+    s = torch.from_numpy(sin)[:, None, :]
+
+    def rot(x):
+        half = d // 2
+        rotated = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+        return (x * c + rotated * s).bfloat16().float().numpy()
+
+    assert np.array_equal(q, rot(t[:, 0]))
+    assert np.array_equal(k, rot(t[:, 1]))
