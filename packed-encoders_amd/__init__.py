@@ -18,7 +18,7 @@ from __future__ import annotations
 
 from . import errors, workloads
 from . import _lib, attention_dispatch, hip_attention
-from . import batch, config, locate, state, ops, pieces, forward, graph, runtime_attention, pack as _pack_module
+from . import batch, config, locate, state, staging, ops, pieces, forward, graph, runtime_attention, pack as _pack_module
 from .batch import PackedBatch
 from .errors import PackedEncodersError, UnsupportedTargetError, ValidationError
 from .forward import packed_forward

@@ -227,11 +227,20 @@ def prologue(model: nn.Module, params: ModernBertParams, input_ids: Tensor, atte
 # ----------------------------------------------------------------------------- packed path
 
 
-def unpad(x: Tensor, attention_mask: Tensor) -> tuple[Tensor, Tensor, Tensor, int, Tensor]:
+def unpad(x: Tensor, attention_mask: Tensor | None) -> tuple[Tensor, Tensor, Tensor, int, Tensor]:
     """Strip padding from ``x [B, S, ...]`` with ``attention_mask [B, S]`` (1 = real token):
     packed rows, their flat ``indices`` (for re-padding), int32 ``cu_seqlens``, ``max_seqlen``
-    (one host read) and ``position_ids = indices % S`` — the token's column, which is the RoPE
-    position Hugging Face ModernBERT gives it (forward.py:395-415)."""
+    and ``position_ids = indices % S`` — the token's column, which is the RoPE position
+    Hugging Face ModernBERT gives it (forward.py:395-415).
+
+    Synchronisation: a device mask costs two device-to-host reads, as in the reference (the
+    packed length and ``max_seqlen``). A host mask with device ``x`` costs none: the layout is
+    built on the host and staged in one pinned non-blocking copy (``staging``). No mask (every
+    token real) costs none either: the layout is a set of device ``arange``s."""
+    if attention_mask is None:
+        return _unpad_dense(x)
+    if attention_mask.device.type == "cpu" and x.device.type == "cuda":
+        return _unpad_host_mask(x, attention_mask)
     b, s = attention_mask.shape
     seqlens = attention_mask.sum(dim=1, dtype=torch.int32)
     indices = torch.nonzero(attention_mask.flatten(), as_tuple=False).flatten()
@@ -239,6 +248,24 @@ def unpad(x: Tensor, attention_mask: Tensor) -> tuple[Tensor, Tensor, Tensor, in
     max_seqlen = int(seqlens.max())
     packed = x.reshape(b * s, *x.shape[2:]).index_select(0, indices)
     return packed, indices, cu_seqlens, max_seqlen, indices % s
+
+
+def _unpad_dense(x: Tensor) -> tuple[Tensor, Tensor, Tensor, int, Tensor]:
+    b, s = x.shape[:2]
+    dev = x.device
+    indices = torch.arange(b * s, device=dev)
+    cu_seqlens = torch.arange(0, (b + 1) * s, s, dtype=torch.int32, device=dev)
+    return x.reshape(b * s, *x.shape[2:]), indices, cu_seqlens, s, indices % s
+
+
+def _unpad_host_mask(x: Tensor, attention_mask: Tensor) -> tuple[Tensor, Tensor, Tensor, int, Tensor]:
+    from .staging import padded_layout_host, stager_for
+
+    b, s = attention_mask.shape
+    indices, cu, positions, max_seqlen = padded_layout_host(attention_mask)
+    d_indices, d_cu, d_positions = stager_for(x.device).put([indices, cu, positions])
+    packed = x.reshape(b * s, *x.shape[2:]).index_select(0, d_indices)
+    return packed, d_indices, d_cu.to(torch.int32), max_seqlen, d_positions
 
 
 def repad(x_packed: Tensor, indices: Tensor, b: int, s: int) -> Tensor:
@@ -310,9 +337,10 @@ def packed_sdpa_fallback(model: nn.Module, params: ModernBertParams, packed_ids:
     return out.reshape(-1, out.shape[-1]).index_select(0, flat)
 
 
-def varlen_forward(model: nn.Module, params: ModernBertParams, input_ids: Tensor, attention_mask: Tensor, *,
+def varlen_forward(model: nn.Module, params: ModernBertParams, input_ids: Tensor, attention_mask: Tensor | None, *,
                    backend: str = "hip", execution=None) -> Tensor:
-    """Padded batch through the packed path: ``unpad`` → ``packed_forward`` → ``repad``."""
+    """Padded batch through the packed path: ``unpad`` → ``packed_forward`` → ``repad``
+    (``attention_mask`` None: every token is real)."""
     b, s = input_ids.shape
     ids, indices, cu, max_seqlen, positions = unpad(input_ids, attention_mask)
     out = packed_forward(model, params, ids, cu, max_seqlen, positions, backend=backend, execution=execution,
@@ -328,8 +356,6 @@ def fused_forward(model: nn.Module, params: ModernBertParams, input_ids: Tensor,
     dtype = model.embeddings.tok_embeddings.weight.dtype
     resolved = resolve_backend(backend, params, device=input_ids.device, dtype=dtype)
     if resolved == "hip":
-        if attention_mask is None:
-            attention_mask = torch.ones_like(input_ids)
         return varlen_forward(model, params, input_ids, attention_mask, backend=resolved, execution=execution)
     p = prologue(model, params, input_ids, attention_mask, execution=execution)
     return core(model, params, p.x, p.cos_global, p.sin_global, p.cos_local, p.sin_local, p.full_mask,

@@ -95,6 +95,35 @@ def test_unpad_repad_roundtrip_and_identity_order():
     assert packed.shape == (6, 5) and cu.tolist() == [0, 3, 6] and positions.tolist() == [0, 1, 2, 0, 1, 2]
 
 
+def test_host_layouts_match_the_device_style_unpad():
+    """staging.padded_layout_host (the sync-free path's layout) equals what unpad computes from
+    the same mask, for right padding, holes, left padding and empty rows; packed_layout_host
+    restarts positions per sequence."""
+    from packed_encoders_amd import staging
+
+    g = torch.Generator().manual_seed(3)
+    masks = [torch.tensor([[1, 1, 1, 0, 0], [1, 1, 1, 1, 1], [0, 0, 0, 0, 0], [0, 1, 1, 0, 1]]),
+             (torch.rand(6, 9, generator=g) > 0.4).long()]
+    for am in masks:
+        x = torch.randn(*am.shape, 3, generator=g)
+        _, want_idx, want_cu, want_max, want_pos = forward.unpad(x, am)
+        idx, cu, pos, mx = staging.padded_layout_host(am)
+        assert torch.equal(idx, want_idx) and torch.equal(cu.to(torch.int32), want_cu)
+        assert torch.equal(pos, want_pos) and mx == want_max
+    cu, pos = staging.packed_layout_host([3, 0, 2, 1])
+    assert cu.tolist() == [0, 3, 3, 5, 6] and pos.tolist() == [0, 1, 2, 0, 1, 0]
+    with pytest.raises(ValueError):
+        staging.padded_layout_host(torch.ones(3, dtype=torch.long))
+
+
+def test_unpad_without_a_mask_is_the_identity_layout():
+    x = torch.randn(2, 5, 3)
+    packed, idx, cu, mx, pos = forward.unpad(x, None)
+    assert torch.equal(packed, x.reshape(10, 3)) and idx.tolist() == list(range(10))
+    assert cu.tolist() == [0, 5, 10] and cu.dtype == torch.int32 and mx == 5
+    assert pos.tolist() == [0, 1, 2, 3, 4] * 2
+
+
 def test_packed_sdpa_fallback_repads_and_restores_packed_order(monkeypatch):
     ids = torch.tensor([11, 12, 21, 31, 32, 33])
     cu = torch.tensor([0, 2, 3, 6], dtype=torch.int32)

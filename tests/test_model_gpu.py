@@ -180,3 +180,34 @@ def test_modernbert_base_shape_packed_forward(pe):
     cos = token_cosine(hip, dense)
     assert torch.isfinite(hip).all()
     assert cos.min() >= 0.99 and cos.mean() >= 0.999, (cos.min(), cos.mean())
+
+
+def test_padded_forward_with_a_host_mask_never_synchronises(pe):
+    """A host attention mask takes the staged layout (one pinned non-blocking copy): the padded
+    forward then makes no device-to-host synchronisation (torch's sync debug mode turns one into
+    an error; the device-mask path, which does synchronise, is the negative control) and
+    returns exactly what the device-mask path returns. No mask at all is sync-free too."""
+    announce("host-mask forward without syncs")
+    model = make_model().cuda().to(torch.bfloat16)
+    pe.pack(model, attention_backend="hip", validate=False)
+    ids, mask = batch([300, 37, 129, 5, 64], seed=11)
+    mask_host = mask.cpu()
+    with torch.no_grad():
+        want = model(input_ids=ids, attention_mask=mask).last_hidden_state
+        model(input_ids=ids, attention_mask=mask_host)  # warm-up: allocations, library load
+        torch.cuda.synchronize()
+        torch.cuda.set_sync_debug_mode("error")
+        try:
+            got = model(input_ids=ids, attention_mask=mask_host).last_hidden_state
+            dense = model(input_ids=ids).last_hidden_state
+            # negative control: the device-mask path's syncs are caught by the same mode
+            with pytest.raises(RuntimeError):
+                model(input_ids=ids, attention_mask=mask)
+        finally:
+            torch.cuda.set_sync_debug_mode(0)
+        torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    with torch.no_grad():
+        dense_want = model(input_ids=ids, attention_mask=torch.ones_like(ids)).last_hidden_state
+    assert torch.equal(dense, dense_want)
+    pe.unpack(model)
