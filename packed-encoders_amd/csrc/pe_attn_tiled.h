@@ -33,9 +33,10 @@
 // Softmax: online, fp32, log2 domain, with a running maximum m that is only a reference
 // point: numerator and denominator share it, so any m gives the same result as long as
 // nothing overflows. Maxima are computed on a query tile's first key tile (and while some row
-// of the wave has seen no key yet); later tiles skip them, and a block whose probabilities
+// of the wave has seen no key yet); later tiles skip them, and a key tile whose probabilities
 // under the stale m sum past 2^64 on some row (scores jumping by more than ~60 in log2 units)
-// is re-scored exactly, raising m and rescaling the accumulators. Probabilities are rounded to
+// is scored again exactly, raising m and rescaling the accumulators before any of it is
+// added. Probabilities are rounded to
 // bf16 for the P.V MFMA, and the row sums add exactly those bf16 values in fp32 (v_dot2 with
 // ones), so numerator and denominator weigh every key alike; the reference sums the unrounded
 // fp32 values (packed_encoders/_kernels/triton_packed_attention.py:122-136), a difference far
@@ -286,90 +287,93 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
                 // Every block of the tile live and unmasked for all of this wave's rows: the
                 // common case, taken without any per-block test.
                 const bool full = (kt0 + BN <= L) && (wl < 0 || (wr1 - 1) - kt0 <= wl) && (wr < 0 || (kt0 + BN - 1) - r0 <= wr);
-                f32x16 s[NB];
-                bool live[NB];
-                // Raw scores S^T = K . Q^T of 32-key block b, -inf outside the rows' windows.
-                auto scores = [&](int b) {
-                    const int kb0 = kt0 + 32 * b;
-                    f32x16 acc;
+                // (Kept as a lambda: the register allocator then fits the step in 136-148 VGPRs;
+                // written inline the same code spills.)
+                auto kv_step = [&]() {
+                    bool live[NB];
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+                    for (int b = 0; b < NB; ++b) live[b] = full || block_live(kt0 + 32 * b, L, r0, wr1, wl, wr);
+                    f32x16 s[NB];
+                    bf16x8 pb[NB][2];
+                    float st[4];
+                    // The running maximum m is only a reference point: numerator and denominator
+                    // share it, so any m gives the same result as long as nothing overflows.
+                    // Maxima are therefore computed only while some row of the wave lacks a
+                    // finite m (the first tiles of a query tile), or when this tile's
+                    // probabilities under the stale m sum past kOverflowGuard on some row: the
+                    // tile is then scored again exactly, m raised and the accumulators rescaled
+                    // before any of it is added (a rare second pass). Otherwise a step spends no
+                    // VALU on maxima.
+                    bool exact = need_exact;
+                    while (true) {
 #pragma unroll
-                    for (int c = 0; c < DC; ++c) acc = mfma32(ld_s16(kt + 32 * b * D + kbase_c[c]), qf[c], acc);
-                    if (!full && !block_full(kb0, L, r0, wr1, wl, wr)) {
-                        const uint32_t km = key_mask(kb0, kg, myrow, L, wl, wr);
+                        for (int b = 0; b < NB; ++b) {
+                            if (!live[b]) continue;
+                            // S^T = K . Q^T of 32-key block b, -inf outside the rows' windows
+                            const int kb0 = kt0 + 32 * b;
+                            f32x16 acc;
 #pragma unroll
-                        for (int j = 0; j < 16; ++j) acc[j] = mask_score(acc[j], km, acc_key(j, 0));
-                    }
-                    s[b] = acc;
-                };
+                            for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
 #pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    live[b] = full || block_live(kt0 + 32 * b, L, r0, wr1, wl, wr);
-                    if (live[b]) scores(b);
-                }
-                // The running maximum m is only a reference point: numerator and denominator
-                // share it, so any m gives the same result as long as nothing overflows. Maxima
-                // are therefore computed only while some row of the wave lacks a finite m (the
-                // first tiles of a query tile), or for a block whose probabilities under the
-                // stale m sum past kOverflowGuard on some row: that block is scored again and m
-                // raised (a rare exact pass). Otherwise a step spends no VALU on maxima.
-                auto raise_max = [&](int b_lo, int b_hi) {
-                    float mp[4] = {kNegInf, kNegInf, kNegInf, kNegInf};  // partial maxima (4 chains)
+                            for (int c = 0; c < DC; ++c) acc = mfma32(ld_s16(kt + 32 * b * D + kbase_c[c]), qf[c], acc);
+                            if (!full && !block_full(kb0, L, r0, wr1, wl, wr)) {
+                                const uint32_t km = key_mask(kb0, kg, myrow, L, wl, wr);
 #pragma unroll
-                    for (int b = 0; b < NB; ++b)
-                        if (b >= b_lo && b < b_hi && live[b]) {
-#pragma unroll
-                            for (int j = 0; j < 16; ++j) mp[j & 3] = fmaxf(mp[j & 3], s[b][j]);
+                                for (int j = 0; j < 16; ++j) acc[j] = mask_score(acc[j], km, acc_key(j, 0));
+                            }
+                            s[b] = acc;
                         }
-                    // Each lane tests its own maximum: the two lanes of a query row share m, so
-                    // "some lane exceeds m" is "some row exceeds m"; only a rescale combines the
-                    // pair.
-                    const float mx = fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]));
-                    if (wave_any(mx * c2 > m + kLazyRescale)) {
-                        const float mnew = fmaxf(m, fmaxf(mx, __shfl_xor(mx, 32)) * c2);
-                        const float alpha = mnew == kNegInf ? 1.0f : exp2_fast(m - mnew);
-                        m = mnew;
+                        if (exact) {
+                            float mp[4] = {kNegInf, kNegInf, kNegInf, kNegInf};  // 4 partial-max chains
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) ls[i] *= alpha;
+                            for (int b = 0; b < NB; ++b)
+                                if (live[b]) {
 #pragma unroll
-                        for (int db = 0; db < DB; ++db)
+                                    for (int j = 0; j < 16; ++j) mp[j & 3] = fmaxf(mp[j & 3], s[b][j]);
+                                }
+                            // Each lane tests its own maximum: the two lanes of a query row share
+                            // m, so "some lane exceeds m" is "some row exceeds m"; only a rescale
+                            // combines the pair.
+                            const float mx = fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]));
+                            if (wave_any(mx * c2 > m + kLazyRescale)) {
+                                const float mnew = fmaxf(m, fmaxf(mx, __shfl_xor(mx, 32)) * c2);
+                                const float alpha = mnew == kNegInf ? 1.0f : exp2_fast(m - mnew);
+                                m = mnew;
 #pragma unroll
-                            for (int j = 0; j < 16; ++j) o[db][j] *= alpha;
-                    }
-                };
-                // Probabilities of block b under m: bf16 MFMA operands and their fp32 row sums.
-                auto probs = [&](int b, bf16x8 (&pb)[2], float (&st)[4]) {
-                    const float muse = m == kNegInf ? 0.0f : m;
+                                for (int i = 0; i < 4; ++i) ls[i] *= alpha;
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) s[b][j] = exp2_fast(fmaf(s[b][j], c2, -muse));
+                                for (int db = 0; db < DB; ++db)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) st[i] = 0.0f;
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        pb[h] = to_bf16x8(s[b], 8 * h);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) st[i] = sum2(pb[h], i, st[i]);
-                    }
-                };
-                const bool exact = need_exact;
-                if (exact) {
-                    raise_max(0, NB);
-                    need_exact = wave_any((m == kNegInf) & (myrow < L));
-                }
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    if (live[b]) {
-                        bf16x8 pb[2];
-                        float st[4];
-                        probs(b, pb, st);
-                        if (!exact && wave_any(fmaxf(fmaxf(st[0], st[1]), fmaxf(st[2], st[3])) > kOverflowGuard)) {
-                            scores(b);
-                            raise_max(b, b + 1);
-                            probs(b, pb, st);
+                                    for (int j = 0; j < 16; ++j) o[db][j] *= alpha;
+                            }
                         }
+                        // Probabilities under m: bf16 MFMA operands and fp32 sums of exactly
+                        // those bf16 values.
+                        const float muse = m == kNegInf ? 0.0f : m;
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) ls[i] += st[i];
+                        for (int i = 0; i < 4; ++i) st[i] = 0.0f;
+#pragma unroll
+                        for (int b = 0; b < NB; ++b) {
+                            if (!live[b]) continue;
+                            f32x16 e;
+#pragma unroll
+                            for (int j = 0; j < 16; ++j) e[j] = exp2_fast(fmaf(s[b][j], c2, -muse));
+#pragma unroll
+                            for (int h = 0; h < 2; ++h) {
+                                pb[b][h] = to_bf16x8(e, 8 * h);
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) st[i] = sum2(pb[b][h], i, st[i]);
+                            }
+                        }
+                        if (exact || !wave_any(fmaxf(fmaxf(st[0], st[1]), fmaxf(st[2], st[3])) > kOverflowGuard)) break;
+                        exact = true;
+                    }
+                    if (need_exact) need_exact = wave_any((m == kNegInf) & (myrow < L));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) ls[i] += st[i];
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        if (!live[b]) continue;
 #pragma unroll
                         for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -379,11 +383,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
                                 const bf16x4 lo = tr16(vt + (32 * b + 16 * h) * D + vbase[0][db]);
                                 const bf16x4 hi = tr16(vt + (32 * b + 16 * h) * D + vbase[1][db]);
                                 const bf16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                                o[db] = mfma32(va, pb[h], o[db]);
+                                o[db] = mfma32(va, pb[b][h], o[db]);
                             }
                         }
                     }
-                }
+                };
+                kv_step();
             }
             end_step();
         }
