@@ -9,11 +9,10 @@
 //    element j at key 8*(j/4) + 4*kg + (j%4) of the 32-key block. Every softmax statistic is
 //    therefore a per-lane scalar, combined with the partner lane l ^ 32 only.
 //  * The output is accumulated transposed too, O^T = V^T . P^T: A = 32 dims x 16 keys read
-//    from a transposed V tile in LDS, B = the lane's own probabilities (8 of them), so no
-//    probability ever leaves its register. Keys of every 32-key block of V^T are stored with
-//    bits 2 and 3 of the key index swapped, which makes the 8 keys lane group kg contributes
-//    to one MFMA (keys 4*kg..4*kg+3 and 8+4*kg..8+4*kg+3 of a 16-key half) contiguous.
-//    The MFMA reduces over its K dimension, so any K permutation shared by A and B is exact.
+//    from the row-major V tile in LDS with ds_read_b64_tr_b16 (its 16-lane transpose hands a
+//    lane four keys of one dim per read), B = the lane's own probabilities (8 of them), so no
+//    probability ever leaves its register. The MFMA reduces over its K dimension, so any key
+//    order shared by A and B is exact.
 #pragma once
 
 #include <hip/hip_runtime.h>

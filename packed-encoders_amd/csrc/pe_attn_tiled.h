@@ -157,21 +157,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
         }
         dma_step(lds, off, k_rs, v_rs);
     };
-    // Q offsets are recomputed at each (rare) Q step rather than held in registers: the empty
-    // asm keeps the compiler from hoisting them out of the loop.
+    // Q step geometry: the wave's RQ rows fill its region of the stage, unit j * 64 + lane
+    // holding row r = unit / CPR, global column (unit % CPR) ^ swz(r).
+    int qoff[LPS];
+#pragma unroll
+    for (int j = 0; j < LPS; ++j) {
+        const int u = j * 64 + lane;
+        const int r = u / CPR, ch = (u % CPR) ^ swz<CPR>(r);
+        qoff[j] = r * q_row + ch * 16;
+    }
     auto issue_q = [&](int stage, int qt, int i) {
         const uint32_t qb = ring_base + stage * kStageBytes + wave * kQWaveBytes;
         const int base = (qt * BM + rb * 32 + i * RQ) * q_row;
-        int ql = lane;
-        asm volatile("" : "+v"(ql));
         uint32_t lds[LPS];
         int off[LPS];
 #pragma unroll
         for (int j = 0; j < LPS; ++j) {
-            const int u = j * 64 + ql;
-            const int r = u / CPR, ch = (u % CPR) ^ swz<CPR>(r);
             lds[j] = qb + j * 1024;
-            off[j] = base + r * q_row + ch * 16;
+            off[j] = base + qoff[j];
         }
         dma_step(lds, off, q_rs, q_rs);
     };

@@ -274,6 +274,61 @@ def test_strips_are_bit_identical_and_match_oracle(pe, window, causal):
     _assert_parity(outs[1], want, cu)
 
 
+def _launch(lib, qd, kd, vd, cud, max_seqlen, window, causal, *, gate=None, strip=0, short_max=0):
+    """One pe_varlen_attn_fwd call through the C-ABI into a fresh output (3.0 everywhere)."""
+    from packed_encoders_amd.hip_attention import _args
+
+    out = torch.full(qd.shape, 3.0, dtype=torch.bfloat16, device="cuda")
+    a = _args(qd, kd, vd, out, cud, max_seqlen, 0.125, window[0], window[1], causal, gate, short_max, strip)
+    size = ctypes.c_size_t()
+    assert lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size)) == 0
+    ws = torch.empty(max(size.value, 1), dtype=torch.uint8, device="cuda")
+    assert lib.pe_varlen_attn_fwd(ctypes.byref(a), ws.data_ptr(), size.value,
+                                  torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    return out
+
+
+WINDOW_LENGTHS = [1, 31, 32, 33, 127, 128, 129, 255, 256, 257, 700, 1500, 64, 2]
+WINDOW_CASES = [((64, 64), False), ((0, 0), False), ((1, 0), False), ((127, -1), True), ((63, 65), False),
+                ((100, 28), False), ((0, 128), False), ((31, 33), False), ((128, 0), False), ((5, 3), True)]
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (6, 2)], ids=["mha", "gqa3"])
+@pytest.mark.parametrize("window,causal", WINDOW_CASES, ids=[f"{w[0]}_{w[1]}{'c' if c else ''}" for w, c in WINDOW_CASES])
+def test_bounded_windows_match_oracle(pe, window, causal, hq, hkv):
+    """Bounded windows of every alignment against the 32-key blocks and 128-row query tiles
+    (segment lengths straddle both edges), with one and three query heads per kv head: the
+    tiled kernel matches the oracle, and a strip of three query tiles per workgroup is
+    bit-identical to one-tile workgroups."""
+    from packed_encoders_amd import _lib
+
+    announce(f"bounded window={window} causal={causal} heads={hq}/{hkv}")
+    q, k, v, cu, _ = _inputs(WINDOW_LENGTHS, hq=hq, hkv=hkv, seed=53)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    lib = _lib.library()
+    mx = max(WINDOW_LENGTHS)
+    got = _launch(lib, qd, kd, vd, cud, mx, window, causal)
+    want = _oracle(q, k, v, cu, scale=0.125, window=window, causal=causal)
+    _assert_parity(got, want, cu)
+    assert torch.equal(_launch(lib, qd, kd, vd, cud, mx, window, causal, strip=3), got)
+
+
+@pytest.mark.parametrize("window,causal", [((64, 64), False), ((100, -1), True)], ids=["band64", "causal100"])
+def test_window_gate_and_short_routing(pe, window, causal):
+    """A windowed call with the fused sigmoid gate, short segments routed to the short kernel in
+    the same call, against the oracle."""
+    from packed_encoders_amd import _lib
+
+    announce(f"window gate window={window} causal={causal}")
+    lengths = [300, 17, 129, 64, 1000, 3]
+    q, k, v, cu, gt = _inputs(lengths, hq=4, seed=59, gate=True)
+    qd, kd, vd, cud, gd = _dev(q, k, v, cu, gt)
+    got = _launch(_lib.library(), qd, kd, vd, cud, max(lengths), window, causal, gate=gd, short_max=64)
+    want = _oracle(q, k, v, cu, scale=0.125, window=window, causal=causal, gate=gt)
+    _assert_parity(got, want, cu)
+
+
 @pytest.mark.parametrize("jump", [4.0, 10.0], ids=["below-guard", "past-guard"])
 @pytest.mark.parametrize("window,causal", [((-1, -1), False), ((64, 64), False), ((-1, -1), True)],
                          ids=["global", "band64", "causal"])
