@@ -171,12 +171,12 @@ int launch_short(const AttnParams &p, int d, bool gate, int short_max, hipStream
 }
 
 // Key tile and LDS ring depth per head dim: 48 KB (head_dim 64: three workgroups per CU, two
-// tiles in flight each) or 64 KB (head_dim 128 and 256, whose register budget allows at most
-// two and one workgroups per CU).
+// tiles in flight each), 64 KB (head_dim 128: two workgroups per CU) or 128 KB (head_dim 256,
+// whose registers allow one workgroup per CU: four stages, three tiles in flight).
 template <int D>
 struct TiledShape {
     static constexpr int BN = D >= 256 ? 32 : 64;
-    static constexpr int NS = D == 64 ? 3 : 2;
+    static constexpr int NS = D == 64 ? 3 : (D == 256 ? 4 : 2);
 };
 
 template <int D, int G, bool GATE, bool WIN>

@@ -112,6 +112,17 @@ __device__ __forceinline__ float sum2(const bf16x8 &p, int i, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(pair, ones, acc, false);
 }
 
+// p[2i] + p[2i + 1] in fp32, starting a sum: the VOP3P form of v_dot2 with an inline zero
+// accumulator, which needs no register cleared beforehand (the compiler selects the
+// accumulating VOP2 form, v_dot2c, and clears its destination with a separate move).
+__device__ __forceinline__ float sum2_first(const bf16x8 &p, int i) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 pair = {p[2 * i], p[2 * i + 1]};
+    float r;
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(pair), "s"(0x3f803f80u));
+    return r;
+}
+
 // Bits lo..hi (clamped to 0..31) of a 32-bit mask; 0 when the range is empty. lo >= 0.
 __device__ __forceinline__ uint32_t bit_range(int lo, int hi) {
     hi = min(hi, 31);
@@ -156,7 +167,10 @@ __device__ __forceinline__ bool block_full(int kb0, int L, int r0, int r1, int w
 
 // Round 4 fp32 outputs to bf16 and apply the optional fused sigmoid gate (g holds the gate's
 // 4 bf16 values): y = bf16(bf16(o) * bf16(sigmoid(g))), the rounding order of the reference's
-// gate kernel (packed_encoders/_kernels/hybrid.py:197-206).
+// gate kernel (packed_encoders/_kernels/hybrid.py:197-206). The sigmoid's reciprocal is
+// v_rcp_f32 (1 ulp) rather than an IEEE division (about ten instructions): its result is
+// rounded to bf16 next, which a 1-ulp fp32 difference can move by one bf16 step only when the
+// quotient lies within that ulp of a rounding boundary.
 template <bool GATE>
 __device__ __forceinline__ bf16x4 out4(float a0, float a1, float a2, float a3, bf16x4 g) {
     bf16x4 r;
@@ -167,7 +181,7 @@ __device__ __forceinline__ bf16x4 out4(float a0, float a1, float a2, float a3, b
     if constexpr (GATE) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float sg = (float)(__bf16)(1.0f / (1.0f + __expf(-(float)g[i])));
+            const float sg = (float)(__bf16)__builtin_amdgcn_rcpf(1.0f + __expf(-(float)g[i]));
             r[i] = (__bf16)((float)r[i] * sg);
         }
     }

@@ -278,6 +278,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
 #pragma unroll
             for (int j = 0; j < 16; ++j) o[db][j] = 0.0f;
         float m = kNegInf;
+        float nmuse = 0.0f;  // -m, or 0 while m is -inf (a row with no key: every p is 0)
         float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         bool need_exact = true;  // some row of the wave may still lack a finite running maximum
 
@@ -342,6 +343,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
                                 const float mnew = fmaxf(m, fmaxf(mx, __shfl_xor(mx, 32)) * c2);
                                 const float alpha = mnew == kNegInf ? 1.0f : exp2_fast(m - mnew);
                                 m = mnew;
+                                nmuse = mnew == kNegInf ? 0.0f : -mnew;
 #pragma unroll
                                 for (int i = 0; i < 4; ++i) ls[i] *= alpha;
 #pragma unroll
@@ -352,7 +354,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
                         }
                         // Probabilities under m: bf16 MFMA operands and fp32 sums of exactly
                         // those bf16 values.
-                        const float muse = m == kNegInf ? 0.0f : m;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) st[i] = 0.0f;
 #pragma unroll
@@ -360,12 +361,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
                             if (!live[b]) continue;
                             f32x16 e;
 #pragma unroll
-                            for (int j = 0; j < 16; ++j) e[j] = exp2_fast(fmaf(s[b][j], c2, -muse));
+                            for (int j = 0; j < 16; ++j) e[j] = exp2_fast(fmaf(s[b][j], c2, nmuse));
 #pragma unroll
                             for (int h = 0; h < 2; ++h) {
                                 pb[b][h] = to_bf16x8(e, 8 * h);
 #pragma unroll
-                                for (int i = 0; i < 4; ++i) st[i] = sum2(pb[b][h], i, st[i]);
+                                for (int i = 0; i < 4; ++i)
+                                    st[i] = (b == 0 && h == 0) ? sum2_first(pb[b][h], i) : sum2(pb[b][h], i, st[i]);
                             }
                         }
                         if (exact || !wave_any(fmaxf(fmaxf(st[0], st[1]), fmaxf(st[2], st[3])) > kOverflowGuard)) break;
