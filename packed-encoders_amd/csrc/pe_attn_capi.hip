@@ -183,7 +183,10 @@ template <int D, int G, bool GATE, bool WIN>
 int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
     constexpr int BN = TiledShape<D>::BN, NS = TiledShape<D>::NS;
     p.hgroups = p.hq / G;
-    const int64_t blocks = cap * p.hgroups;
+    // Banded head_dim 64 launches deal work to the 8 XCDs in runs (tiled_attn_kernel): whole
+    // rounds of runs, the surplus workgroups exiting at once.
+    const int64_t run = 8LL * pe::kXcdRun * p.hgroups;
+    const int64_t blocks = (D == 64 && WIN) ? (cap * p.hgroups + run - 1) / run * run : cap * p.hgroups;
     if (blocks <= 0) return PE_ATTN_OK;
     if (blocks > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
     if constexpr (D == 64)

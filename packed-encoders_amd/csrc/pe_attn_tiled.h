@@ -56,6 +56,9 @@ constexpr float kLazyRescale = 8.0f;  // log2 of the largest unnormalised probab
 // Largest per-row, per-tile probability sum accepted under a stale running maximum (2^64: far
 // from overflowing the bf16 probabilities, the fp32 sums or the fp32 P.V accumulators).
 constexpr float kOverflowGuard = 18446744073709551616.0f;
+// Consecutive work entries (all head groups of each) that one XCD takes in a row in banded
+// calls, so that neighbouring query tiles meet in one L2.
+constexpr int kXcdRun = 4;
 
 // WIN: the call has a window or causal bound. Without one (global attention) every window
 // test folds away at compile time, which also gives global and windowed launches distinct
@@ -80,9 +83,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
 
     __shared__ __attribute__((aligned(16))) __bf16 ring[NS][2][TILE];
 
-    const int entry = blockIdx.x / p.hgroups;
-    const int hg = blockIdx.x - entry * p.hgroups;
-    if (entry >= *p.work_count) return;
+    // Work item of this workgroup: the list walked with the head group fastest, so that the
+    // costliest strips of every head go first and the heads of one query tile, which read
+    // adjacent 128-byte pieces of the same token rows, run together. Workgroup i runs on XCD
+    // i % 8; a banded call re-reads each key block from the neighbouring query tile's
+    // workgroups, so it deals the list to the XCDs in runs of kXcdRun entries: neighbours then
+    // share one L2 instead of fetching the shared keys twice, and the dealing keeps the
+    // longest-first order across XCDs (whole contiguous eighths would give one XCD all the
+    // costliest tiles). The launch rounds the grid up to whole rounds of runs.
+    const int count = *p.work_count;
+    int item = blockIdx.x;
+    if (WIN && p.wl >= 0 && p.wr >= 0) {
+        const int n = count * p.hgroups;
+        const int rh = kXcdRun * p.hgroups;
+        const int j = (int)(blockIdx.x >> 3);
+        item = ((j / rh) * 8 + (int)(blockIdx.x & 7)) * rh + j % rh;
+        if (item >= n) return;
+    }
+    const int entry = item / p.hgroups;
+    const int hg = item - entry * p.hgroups;
+    if (entry >= count) return;
     const int2 w = p.work[entry];
     const int seg = w.x, qt_first = w.y;
     if (seg < 0 || seg >= p.n_seq || qt_first < 0 || p.strip < 1) return;  // a plan made for other arguments
