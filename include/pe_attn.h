@@ -21,7 +21,9 @@
  *   rounded to bf16. With a gate, out = bf16(bf16(out) * bf16(sigmoid(gate))).
  *   Rows at or beyond cu_seqlens[n_seq] are never written. Empty segments are allowed.
  *   Caller contract (not checked on device): cu_seqlens[0] = 0, non-decreasing,
- *   cu_seqlens[n_seq] <= total_tokens, and max_seqlen >= every segment length.
+ *   cu_seqlens[n_seq] <= total_tokens, and max_seqlen >= every segment length. The kernels'
+ *   32-bit offsets are sized from max_seqlen, so a segment longer than it is skipped (its rows
+ *   are left unwritten) rather than addressed.
  */
 #ifndef PE_ATTN_H
 #define PE_ATTN_H

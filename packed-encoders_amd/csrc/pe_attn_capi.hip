@@ -127,6 +127,7 @@ AttnParams make_params(const pe_attn_args *a, int short_max) {
     p.wr = a->window_right;
     if (a->causal) p.wr = 0;  // causal = no key to the right of the query
     p.short_max = short_max;
+    p.max_seqlen = a->max_seqlen;
     p.strip = effective_strip(a);
     p.c = a->softmax_scale * pe::kLog2e;
     return p;

@@ -39,6 +39,7 @@ struct AttnParams {
     int32_t group;   // query heads per kv head
     int32_t wl, wr;  // window (-1: unbounded); causal already folded into wr = 0
     int32_t short_max;
+    int32_t max_seqlen;  // the caller's bound on segment lengths (32-bit offsets were sized for it)
     int32_t hgroups; // head groups per work entry (tiled kernel)
     int32_t strip;   // query tiles per work entry (tiled kernel)
     float c;         // softmax_scale * log2(e)

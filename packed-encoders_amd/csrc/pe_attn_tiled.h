@@ -108,6 +108,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
     if (seg < 0 || seg >= p.n_seq || qt_first < 0 || p.strip < 1) return;  // a plan made for other arguments
     const int start = p.cu[seg];
     const int L = p.cu[seg + 1] - start;
+    // A segment longer than the caller's max_seqlen breaks the contract the host sized the
+    // 32-bit buffer offsets by: its rows are left unwritten rather than addressed.
+    if (L > p.max_seqlen) return;
     const int nq = (L + BM - 1) / BM;
     if (qt_first >= nq) return;
     const int qt_end = min(nq, qt_first + p.strip);

@@ -221,6 +221,28 @@ def test_rows_beyond_last_boundary_and_empty_segments_untouched(pe):
         _assert_parity(out, want, cu.cpu())
 
 
+@pytest.mark.parametrize("d", [64, 256])
+def test_segment_longer_than_max_seqlen_is_skipped(pe, d):
+    """max_seqlen sizes the kernels' 32-bit offsets; a segment longer than the caller's bound
+    breaches that contract and is left unwritten instead of being addressed, while the other
+    segments of the call are computed as usual."""
+    from packed_encoders_amd import _lib
+
+    announce(f"segment longer than max_seqlen d={d}")
+    lengths = [100, 300, 150]
+    q, k, v, cu, _ = _inputs(lengths, hq=4, hkv=4 if d == 64 else 1, d=d, seed=61)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    out = _launch(_lib.library(), qd, kd, vd, cud, 200, (-1, -1), False)
+    assert torch.all(out[100:400] == 3.0)
+    want = _oracle(q, k, v, cu, scale=0.125)
+    keep = torch.ones(sum(lengths), dtype=torch.bool)
+    keep[100:400] = False
+    idx = keep.nonzero().flatten()
+    got = out.float().cpu()[idx]
+    sub_cu = torch.tensor([0, 100, 250], dtype=torch.int32)
+    _assert_parity(got, want[idx.numpy()], sub_cu)
+
+
 def test_workspace_too_small_is_reported(pe):
     from packed_encoders_amd import _lib
     from packed_encoders_amd.hip_attention import _args
