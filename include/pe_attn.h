@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define PE_ATTN_ABI_VERSION 3
+#define PE_ATTN_ABI_VERSION 4
 
 #define PE_ATTN_OK 0
 #define PE_ATTN_EINVAL (-1)       /* malformed arguments (maps to ValueError) */
@@ -81,6 +81,17 @@ typedef struct pe_attn_args {
        workgroup of the tiled kernel walks in sequence, its key/value pipeline running across
        tile boundaries. 0 asks for the library's default; at most 64. */
     int32_t strip;
+    /* Key/value segments distinct from the query segments (FlashAttention's cu_seqlens_k):
+       device [n_seq + 1], or NULL for the query segments themselves (then the two fields
+       below are ignored). k and v hold total_tokens_k rows. Query segment s is the TAIL of key
+       segment s: its row r sits at key position r + (Lk - Lq), and the causal bound and the
+       window are measured from there (the reference's prefixed form for rows continuing a
+       shared prefix, packed_encoders/runtime/attention.py:15-19,236-245; flash_attn_varlen's
+       bottom-right alignment). A row that reaches no key comes out as zero. Segments with both
+       lengths <= short_max take the short kernel. */
+    const int32_t *cu_seqlens_k;
+    int32_t total_tokens_k;
+    int32_t max_seqlen_k; /* host bound on every key segment length */
 } pe_attn_args;
 
 /* ABI version of the loaded library; callers compare it with PE_ATTN_ABI_VERSION. */

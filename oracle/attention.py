@@ -15,7 +15,9 @@ fp32/fp64 per-segment dense softmax attention, confined to each segment's
 Parity pins (tests/test_oracle.py): the brute-force loop form below on tiny inputs, closed
 forms (L = 1 and half = 0 give v; q = 0 gives the window mean of v; Hkv = Hq GQA equals MHA;
 half >= L - 1 equals global), bf16 rounding against torch's, and the reference's own compiled
-CPU kernel (oracle/_ref) at fp32 tolerance.
+CPU kernel (oracle/_ref) at fp32 tolerance. Separate key segments (queries the tail of their
+keys) are pinned by the brute-force form and by the tail identity: they must equal the last
+rows of self-attention over the whole key segment.
 """
 
 from __future__ import annotations
@@ -56,38 +58,48 @@ def allowed_mask(n_q: int, n_k: int, window=(-1, -1), causal: bool = False) -> n
 
 
 def segment_attention(q, k, v, *, scale: float, window=(-1, -1), causal: bool = False) -> np.ndarray:
-    """One segment: q ``[L, Hq, D]``, k/v ``[L, Hkv, D]`` → float64 ``[L, Hq, D]``."""
+    """One segment: q ``[Lq, Hq, D]``, k/v ``[Lk, Hkv, D]`` → float64 ``[Lq, Hq, D]``. With
+    ``Lk != Lq`` the queries are the last ``Lq`` of the ``Lk`` key positions (the reference's
+    prefixed form, runtime/attention.py:157-170,236-245); a query that may read no key gets
+    zeros (FlashAttention's convention; SDPA would give NaN)."""
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
     v = np.asarray(v, dtype=np.float64)
     n, hq, _ = q.shape
-    hkv = k.shape[1]
+    nk, hkv = k.shape[0], k.shape[1]
     if n == 0:
+        return np.zeros_like(q)
+    if nk == 0:
         return np.zeros_like(q)
     group = hq // hkv
     kr = np.repeat(k, group, axis=1)  # kv head h // group serves query head h
     vr = np.repeat(v, group, axis=1)
     scores = np.einsum("qhd,khd->hqk", q, kr) * scale
-    mask = allowed_mask(n, n, window, causal)
+    mask = allowed_mask(n, nk, window, causal)
     scores = np.where(mask[None], scores, -np.inf)
     mx = scores.max(axis=-1, keepdims=True)
-    p = np.exp(scores - mx)
-    p /= p.sum(axis=-1, keepdims=True)
+    empty = ~np.isfinite(mx)
+    p = np.exp(scores - np.where(empty, 0.0, mx))
+    total = p.sum(axis=-1, keepdims=True)
+    p = p / np.where(empty, 1.0, total)
     return np.einsum("hqk,khd->qhd", p, vr)
 
 
 def packed_attention(q, k, v, cu_seqlens, *, scale: float, window=(-1, -1), causal: bool = False,
-                     gate=None) -> np.ndarray:
+                     gate=None, cu_seqlens_k=None) -> np.ndarray:
     """Packed varlen attention over ``[T, H, D]`` arrays; rows outside every segment are NaN.
 
-    With ``gate`` the result is the gated output computed from the bf16-rounded attention
-    output, exactly as the reference's separate gate kernel consumes it."""
+    ``cu_seqlens_k`` gives k/v segments of their own (query segment s reads key segment s, its
+    queries the tail of those positions); by default the query segments. With ``gate`` the
+    result is the gated output computed from the bf16-rounded attention output, exactly as
+    the reference's separate gate kernel consumes it."""
     cu = [int(x) for x in np.asarray(cu_seqlens).tolist()]
+    cuk = cu if cu_seqlens_k is None else [int(x) for x in np.asarray(cu_seqlens_k).tolist()]
     q = np.asarray(q)
     out = np.full(q.shape, np.nan, dtype=np.float64)
-    for a, b in zip(cu, cu[1:]):
+    for (a, b), (ka, kb) in zip(zip(cu, cu[1:]), zip(cuk, cuk[1:])):
         if b > a:
-            out[a:b] = segment_attention(q[a:b], k[a:b], v[a:b], scale=scale, window=window, causal=causal)
+            out[a:b] = segment_attention(q[a:b], k[ka:kb], v[ka:kb], scale=scale, window=window, causal=causal)
     if gate is not None:
         out = sigmoid_gate(to_bf16(out), gate)
     return out
@@ -129,22 +141,32 @@ def sampled_rows_attention(q, k, v, cu_seqlens, rows, *, scale: float, window=(-
     return out
 
 
-def brute_force_attention(q, k, v, cu_seqlens, *, scale: float, window=(-1, -1), causal: bool = False):
+def brute_force_attention(q, k, v, cu_seqlens, *, scale: float, window=(-1, -1), causal: bool = False,
+                          cu_seqlens_k=None):
     """Scalar-loop float64 form of the same semantics, for tiny inputs only: every score, max,
-    exponential and weighted sum written out, with no vectorised masking or broadcasting."""
+    exponential and weighted sum written out, with no vectorised masking or broadcasting. A
+    query of segment [a, b) with key segment [ka, kb) sits at key position
+    (i - a) + (kb - ka) - (b - a); a query that reaches no key gets zeros."""
     cu = [int(x) for x in np.asarray(cu_seqlens).tolist()]
+    cuk = cu if cu_seqlens_k is None else [int(x) for x in np.asarray(cu_seqlens_k).tolist()]
     T, hq, d = np.asarray(q).shape
     hkv = np.asarray(k).shape[1]
     left, right = window
     if causal:
         right = 0
     out = [[[math.nan] * d for _ in range(hq)] for _ in range(T)]
-    for a, b in zip(cu, cu[1:]):
+    for (a, b), (ka, kb) in zip(zip(cu, cu[1:]), zip(cuk, cuk[1:])):
+        shift = (kb - ka) - (b - a)
         for h in range(hq):
             kvh = h // (hq // hkv)
             for i in range(a, b):
-                keys = [j for j in range(a, b)
-                        if (left < 0 or (i - a) - (j - a) <= left) and (right < 0 or (j - a) - (i - a) <= right)]
+                pos = (i - a) + shift
+                keys = [j for j in range(ka, kb)
+                        if (left < 0 or pos - (j - ka) <= left) and (right < 0 or (j - ka) - pos <= right)]
+                if not keys:
+                    for x in range(d):
+                        out[i][h][x] = 0.0
+                    continue
                 scores = []
                 for j in keys:
                     acc = 0.0

@@ -12,7 +12,7 @@ from pathlib import Path
 
 from ._build import LIBRARY
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 DTYPE_BF16 = 1
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH = 0, -1, -2, -3, -4
@@ -65,6 +65,9 @@ class AttnArgs(ctypes.Structure):
         ("causal", ctypes.c_int32),
         ("short_max", ctypes.c_int32),
         ("strip", ctypes.c_int32),
+        ("cu_seqlens_k", ctypes.c_void_p),
+        ("total_tokens_k", ctypes.c_int32),
+        ("max_seqlen_k", ctypes.c_int32),
     ]
 
 

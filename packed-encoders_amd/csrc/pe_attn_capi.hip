@@ -48,6 +48,7 @@ int check_args(const pe_attn_args *a, bool need_pointers = true) {
     if (a->causal != 0 && a->causal != 1) return PE_ATTN_EINVAL;
     if (a->short_max < -1 || a->short_max > 128) return PE_ATTN_EINVAL;
     if (a->strip < 0 || a->strip > kMaxStrip) return PE_ATTN_EINVAL;
+    if (a->cu_seqlens_k && (a->total_tokens_k < 0 || a->max_seqlen_k < 0)) return PE_ATTN_EINVAL;
     if (!need_pointers || a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
     if (!a->q || !a->k || !a->v || !a->o || !a->cu_seqlens) return PE_ATTN_EINVAL;
     const void *ptrs[4] = {a->q, a->k, a->v, a->o};
@@ -64,11 +65,16 @@ int check_args(const pe_attn_args *a, bool need_pointers = true) {
     }
     // Kernels address a segment through 32-bit buffer offsets bounded by its last row: rows
     // must not overlap (token stride >= head_dim) and a segment must span < 2 GiB per tensor.
+    const int64_t kv_rows = a->cu_seqlens_k ? a->total_tokens_k : a->total_tokens;
+    const int64_t kv_max = a->cu_seqlens_k ? a->max_seqlen_k : a->max_seqlen;
     const int64_t token_strides[5] = {a->q_stride_token, a->k_stride_token, a->v_stride_token, a->o_stride_token,
                                       a->gate ? a->gate_stride_token : a->head_dim};
-    for (int64_t s : token_strides) {
-        if (a->total_tokens > 1 && s < a->head_dim) return PE_ATTN_EINVAL;
-        if ((int64_t)a->max_seqlen * s * 2 + 2 * a->head_dim >= (int64_t)1 << 31) return PE_ATTN_EUNSUPPORTED;
+    for (int i = 0; i < 5; ++i) {
+        const int64_t s = token_strides[i];
+        const bool kv = i == 1 || i == 2;
+        if ((kv ? kv_rows : a->total_tokens) > 1 && s < a->head_dim) return PE_ATTN_EINVAL;
+        if ((kv ? kv_max : (int64_t)a->max_seqlen) * s * 2 + 2 * a->head_dim >= (int64_t)1 << 31)
+            return PE_ATTN_EUNSUPPORTED;
     }
     return PE_ATTN_OK;
 }
@@ -85,9 +91,12 @@ int heads_per_tile(const pe_attn_args *a) { return gcd_int(a->n_heads_q / a->n_h
 // Upper bound on (segment, strip) entries the plan can emit, from host-known sizes only:
 // a segment of L > short_max tokens has ceil(L / bm) query tiles in ceil(tiles / strip) strips.
 int64_t tile_capacity(const pe_attn_args *a, int short_max, int bm, int strip) {
-    if (a->n_seq == 0 || a->total_tokens == 0 || a->max_seqlen <= short_max) return 0;
+    const int32_t max_k = a->cu_seqlens_k ? a->max_seqlen_k : a->max_seqlen;
+    if (a->n_seq == 0 || a->total_tokens == 0 || (a->max_seqlen <= short_max && max_k <= short_max)) return 0;
     const int64_t n = a->n_seq, t = a->total_tokens;
-    const int64_t n_long = short_max > 0 ? (t / (short_max + 1) < n ? t / (short_max + 1) : n) : n;
+    // With separate key segments a segment of few queries can still be long (its keys): every
+    // segment may then reach the tiled kernel.
+    const int64_t n_long = short_max > 0 && !a->cu_seqlens_k ? (t / (short_max + 1) < n ? t / (short_max + 1) : n) : n;
     const int64_t tiles_per_seg = (a->max_seqlen + bm - 1) / bm;
     const int64_t by_shape = n * ((tiles_per_seg + strip - 1) / strip);
     const int64_t tiles_by_tokens = (t + n_long * (bm - 1)) / bm;
@@ -110,6 +119,7 @@ AttnParams make_params(const pe_attn_args *a, int short_max) {
     p.g = static_cast<const __bf16 *>(a->gate);
     p.o = static_cast<__bf16 *>(a->o);
     p.cu = a->cu_seqlens;
+    p.cuk = a->cu_seqlens_k ? a->cu_seqlens_k : a->cu_seqlens;
     p.q_st = a->q_stride_token;
     p.q_sh = a->q_stride_head;
     p.k_st = a->k_stride_token;
@@ -128,6 +138,7 @@ AttnParams make_params(const pe_attn_args *a, int short_max) {
     if (a->causal) p.wr = 0;  // causal = no key to the right of the query
     p.short_max = short_max;
     p.max_seqlen = a->max_seqlen;
+    p.max_seqlen_k = a->cu_seqlens_k ? a->max_seqlen_k : a->max_seqlen;
     p.strip = effective_strip(a);
     p.c = a->softmax_scale * pe::kLog2e;
     return p;
@@ -294,8 +305,9 @@ int pe_attn_plan(const pe_attn_args *a, void *workspace, size_t workspace_bytes,
     int32_t *count = static_cast<int32_t *>(workspace);
     int2 *work = reinterpret_cast<int2 *>(static_cast<char *>(workspace) + kWorkspaceHeader);
     const int wr = a->causal ? 0 : a->window_right;
-    hipLaunchKernelGGL(pe::plan_kernel, dim3(1), dim3(1024), 0, stream, a->cu_seqlens, a->n_seq, plan.sm, plan.bm,
-                       plan.strip, a->window_left, wr, work, count, (int)plan.cap);
+    hipLaunchKernelGGL(pe::plan_kernel, dim3(1), dim3(1024), 0, stream, a->cu_seqlens,
+                       a->cu_seqlens_k ? a->cu_seqlens_k : a->cu_seqlens, a->n_seq, plan.sm, plan.bm, plan.strip,
+                       a->window_left, wr, work, count, (int)plan.cap);
     return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
 }
 
@@ -335,13 +347,14 @@ int pe_varlen_attn_fwd(const pe_attn_args *a, void *workspace, size_t workspace_
 int pe_packed_short_attn_fwd(const pe_attn_args *a, hipStream_t stream) {
     int rc = check_args(a, false);
     if (rc) return rc;
-    if (a->max_seqlen <= 0 || a->max_seqlen > 128) return PE_ATTN_EUNSUPPORTED;
+    const int32_t smax = a->cu_seqlens_k && a->max_seqlen_k > a->max_seqlen ? a->max_seqlen_k : a->max_seqlen;
+    if (smax <= 0 || smax > 128) return PE_ATTN_EUNSUPPORTED;
     if (a->head_dim > 128) return PE_ATTN_EUNSUPPORTED;
     rc = check_args(a);
     if (rc) return rc;
     if (a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
-    AttnParams p = make_params(a, a->max_seqlen);
-    return launch_short(p, a->head_dim, a->gate != nullptr, a->max_seqlen, stream);
+    AttnParams p = make_params(a, smax);
+    return launch_short(p, a->head_dim, a->gate != nullptr, smax, stream);
 }
 
 int pe_attn_short_config(int32_t max_seqlen, int32_t head_dim, int32_t out[4]) {

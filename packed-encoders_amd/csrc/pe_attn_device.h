@@ -33,13 +33,15 @@ struct AttnParams {
     const __bf16 *q, *k, *v, *g;
     __bf16 *o;
     const int32_t *cu;
+    const int32_t *cuk;  // key/value segment boundaries (cu when keys and queries share them)
     int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, g_st, g_sh;
     int32_t n_seq;
     int32_t hq;      // query heads
     int32_t group;   // query heads per kv head
     int32_t wl, wr;  // window (-1: unbounded); causal already folded into wr = 0
     int32_t short_max;
-    int32_t max_seqlen;  // the caller's bound on segment lengths (32-bit offsets were sized for it)
+    int32_t max_seqlen;    // the caller's bound on query segment lengths (32-bit offsets were sized for it)
+    int32_t max_seqlen_k;  // and on key segment lengths
     int32_t hgroups; // head groups per work entry (tiled kernel)
     int32_t strip;   // query tiles per work entry (tiled kernel)
     float c;         // softmax_scale * log2(e)
@@ -149,6 +151,10 @@ __device__ __forceinline__ float mask_score(float a, uint32_t m, int x) {
     const int keep = (int)(m << (31 - x)) >> 31;
     return __builtin_bit_cast(float, (__builtin_bit_cast(int, a) & keep) | (~keep & (int)0xff800000));
 }
+
+// Rows passed to the mask helpers below are key positions: query row r of a segment whose key
+// segment is Lk long and query segment Lq long sits at key position r + (Lk - Lq) (queries are
+// the tail of their keys; 0 when both are the same segment).
 
 // Whether key block [kb0, kb0 + 32) intersects the keys any row in [r0, r1) may read.
 __device__ __forceinline__ bool block_live(int kb0, int L, int r0, int r1, int wl, int wr) {

@@ -15,17 +15,20 @@
 
 namespace pe {
 
-__device__ __forceinline__ int plan_tile_cost(int t, int bm, int L, int wl, int wr) {
-    const int r0 = t * bm, r1 = min(L, r0 + bm);
+// Keys query tile t of a segment with L query rows and Lk keys visits (rows end-aligned to
+// the keys: row r sits at key position r + Lk - L).
+__device__ __forceinline__ int plan_tile_cost(int t, int bm, int L, int Lk, int wl, int wr) {
+    const int off = Lk - L;
+    const int r0 = t * bm + off, r1 = min(L, t * bm + bm) + off;
     const int klo = wl >= 0 ? max(0, r0 - wl) : 0;
-    const int khi = wr >= 0 ? min(L, r1 + wr) : L;
+    const int khi = wr >= 0 ? min(Lk, r1 + wr) : Lk;
     return max(1, khi - klo);
 }
 
 // Keys visited by the query tiles [s * strip, min(nq, (s + 1) * strip)) of a segment.
-__device__ __forceinline__ int plan_strip_cost(int s, int strip, int nq, int bm, int L, int wl, int wr) {
+__device__ __forceinline__ int plan_strip_cost(int s, int strip, int nq, int bm, int L, int Lk, int wl, int wr) {
     int64_t cost = 0;
-    for (int t = s * strip; t < min(nq, (s + 1) * strip); ++t) cost += plan_tile_cost(t, bm, L, wl, wr);
+    for (int t = s * strip; t < min(nq, (s + 1) * strip); ++t) cost += plan_tile_cost(t, bm, L, Lk, wl, wr);
     return (int)min(cost, (int64_t)0x7fffffff);
 }
 
@@ -36,19 +39,22 @@ __device__ __forceinline__ int plan_bucket(int cost) {
 }
 
 // One entry per strip of `strip` consecutive query tiles of `bm` rows: (segment, first tile).
-__global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, int n_seq, int short_max, int bm, int strip,
-                                                    int wl, int wr, int2 *work, int32_t *count, int cap) {
+// Segment s has cu[s + 1] - cu[s] query rows and cuk[s + 1] - cuk[s] keys (cuk = cu when the
+// two share boundaries); it is the short kernel's when both fit short_max.
+__global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int32_t *cuk, int n_seq, int short_max,
+                                                    int bm, int strip, int wl, int wr, int2 *work, int32_t *count,
+                                                    int cap) {
     __shared__ int cnt[64];
     __shared__ int off[64];
     const int tid = threadIdx.x;
     if (tid < 64) cnt[tid] = 0;
     __syncthreads();
     for (int seg = tid; seg < n_seq; seg += blockDim.x) {
-        const int L = cu[seg + 1] - cu[seg];
-        if (L <= short_max) continue;
+        const int L = cu[seg + 1] - cu[seg], Lk = cuk[seg + 1] - cuk[seg];
+        if (max(L, Lk) <= short_max) continue;
         const int nq = (L + bm - 1) / bm;
         const int ns = (nq + strip - 1) / strip;
-        for (int s = 0; s < ns; ++s) atomicAdd(&cnt[plan_bucket(plan_strip_cost(s, strip, nq, bm, L, wl, wr))], 1);
+        for (int s = 0; s < ns; ++s) atomicAdd(&cnt[plan_bucket(plan_strip_cost(s, strip, nq, bm, L, Lk, wl, wr))], 1);
     }
     __syncthreads();
     if (tid == 0) {
@@ -61,16 +67,16 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, int n_seq
     }
     __syncthreads();
     for (int seg = tid; seg < n_seq; seg += blockDim.x) {
-        const int L = cu[seg + 1] - cu[seg];
-        if (L <= short_max) continue;
+        const int L = cu[seg + 1] - cu[seg], Lk = cuk[seg + 1] - cuk[seg];
+        if (max(L, Lk) <= short_max) continue;
         const int nq = (L + bm - 1) / bm;
         const int ns = (nq + strip - 1) / strip;
         int s = 0;
         while (s < ns) {
             // A run of consecutive strips in one cost bucket gets one contiguous reservation.
-            const int b = plan_bucket(plan_strip_cost(s, strip, nq, bm, L, wl, wr));
+            const int b = plan_bucket(plan_strip_cost(s, strip, nq, bm, L, Lk, wl, wr));
             int e = s + 1;
-            while (e < ns && plan_bucket(plan_strip_cost(e, strip, nq, bm, L, wl, wr)) == b) ++e;
+            while (e < ns && plan_bucket(plan_strip_cost(e, strip, nq, bm, L, Lk, wl, wr)) == b) ++e;
             const int pos = atomicAdd(&off[b], e - s);
             for (int i = 0; i < e - s; ++i)
                 if (pos + i < cap) work[pos + i] = make_int2(seg, (s + i) * strip);

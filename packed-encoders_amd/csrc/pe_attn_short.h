@@ -38,8 +38,11 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
 
     const int seg = blockIdx.x;
     const int start = p.cu[seg];
-    const int L = p.cu[seg + 1] - start;
-    if (L <= 0 || L > p.short_max) return;
+    const int L = p.cu[seg + 1] - start;  // query rows
+    const int kstart = p.cuk[seg];
+    const int Lk = p.cuk[seg + 1] - kstart;  // keys
+    if (L <= 0 || Lk < 0 || max(L, Lk) > p.short_max) return;
+    const int off = Lk - L;  // key position of query row 0 (queries end-aligned to their keys)
     const int h0 = blockIdx.y * HPW;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -61,7 +64,7 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
     }
 
     // K and V of every head of the group: unit u = (j * 4 + wave) * 64 + lane of a tile holds
-    // key u / CPR, global column (u % CPR) ^ swz(key); keys >= L read as zero.
+    // key u / CPR, global column (u % CPR) ^ swz(key); keys >= Lk read as zero.
     const int k_row = (int)p.k_st * 2, v_row = (int)p.v_st * 2;
     const uint32_t kv_base = uniform((int)lds_addr(&kv[0][0][0]));
 #pragma unroll
@@ -69,8 +72,8 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
         const int h = h0 + hs;
         if (h >= p.hq) break;
         const int kvh = h / p.group;
-        const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(p.k + (int64_t)start * p.k_st + (int64_t)kvh * p.k_sh, rows_bytes(L, p.k_st, D));
-        const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(p.v + (int64_t)start * p.v_st + (int64_t)kvh * p.v_sh, rows_bytes(L, p.v_st, D));
+        const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(p.k + (int64_t)kstart * p.k_st + (int64_t)kvh * p.k_sh, rows_bytes(Lk, p.k_st, D));
+        const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(p.v + (int64_t)kstart * p.v_st + (int64_t)kvh * p.v_sh, rows_bytes(Lk, p.v_st, D));
 #pragma unroll
         for (int j = 0; j < UPT; ++j) {
             const int u = (j * 4 + wave) * 64 + lane;
@@ -104,7 +107,7 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
 
     const int wl = p.wl, wr = p.wr;
     const float c2 = p.c;
-    const int nkb = (L + 31) >> 5;
+    const int nkb = (Lk + 31) >> 5;
     const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(p.o + (int64_t)start * p.o_st + (int64_t)qh * p.o_sh, rows_bytes(L, p.o_st, D));
     __amdgpu_buffer_rsrc_t g_rs = o_rs;
     if constexpr (GATE) g_rs = make_rsrc(p.g + (int64_t)start * p.g_st + (int64_t)qh * p.g_sh, rows_bytes(L, p.g_st, D));
@@ -121,15 +124,15 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             const int kb0 = 32 * b;
-            live[b] = b < nkb && block_live(kb0, L, r0, r1, wl, wr);
+            live[b] = b < nkb && block_live(kb0, Lk, r0 + off, r1 + off, wl, wr);
             if (live[b]) {
                 f32x16 acc;
 #pragma unroll
                 for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
 #pragma unroll
                 for (int c = 0; c < DC; ++c) acc = mfma32(ld_s16(kt + kb0 * D + kbase_c[c]), qf[i][c], acc);
-                if (!block_full(kb0, L, r0, r1, wl, wr)) {
-                    const uint32_t km = key_mask(kb0, kg, myrow, L, wl, wr);
+                if (!block_full(kb0, Lk, r0 + off, r1 + off, wl, wr)) {
+                    const uint32_t km = key_mask(kb0, kg, myrow + off, Lk, wl, wr);
 #pragma unroll
                     for (int j = 0; j < 16; ++j) acc[j] = mask_score(acc[j], km, acc_key(j, 0));
                 }

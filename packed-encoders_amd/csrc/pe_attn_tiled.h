@@ -107,10 +107,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
     const int seg = w.x, qt_first = w.y;
     if (seg < 0 || seg >= p.n_seq || qt_first < 0 || p.strip < 1) return;  // a plan made for other arguments
     const int start = p.cu[seg];
-    const int L = p.cu[seg + 1] - start;
+    const int L = p.cu[seg + 1] - start;  // query rows
+    const int kstart = p.cuk[seg];
+    const int Lk = p.cuk[seg + 1] - kstart;  // keys
     // A segment longer than the caller's max_seqlen breaks the contract the host sized the
     // 32-bit buffer offsets by: its rows are left unwritten rather than addressed.
-    if (L > p.max_seqlen) return;
+    if (L > p.max_seqlen || Lk > p.max_seqlen_k || Lk < 0) return;
+    const int off = Lk - L;  // key position of query row 0 (queries end-aligned to their keys)
     const int nq = (L + BM - 1) / BM;
     if (qt_first >= nq) return;
     const int qt_end = min(nq, qt_first + p.strip);
@@ -125,19 +128,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
     const int wl = WIN ? p.wl : -1, wr = WIN ? p.wr : -1;
 
     const __amdgpu_buffer_rsrc_t q_rs = make_rsrc(p.q + (int64_t)start * p.q_st + (int64_t)qh * p.q_sh, rows_bytes(L, p.q_st, D));
-    const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(p.k + (int64_t)start * p.k_st + (int64_t)kvh * p.k_sh, rows_bytes(L, p.k_st, D));
-    const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(p.v + (int64_t)start * p.v_st + (int64_t)kvh * p.v_sh, rows_bytes(L, p.v_st, D));
+    const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(p.k + (int64_t)kstart * p.k_st + (int64_t)kvh * p.k_sh, rows_bytes(Lk, p.k_st, D));
+    const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(p.v + (int64_t)kstart * p.v_st + (int64_t)kvh * p.v_sh, rows_bytes(Lk, p.v_st, D));
     const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(p.o + (int64_t)start * p.o_st + (int64_t)qh * p.o_sh, rows_bytes(L, p.o_st, D));
     __amdgpu_buffer_rsrc_t g_rs = o_rs;
     if constexpr (GATE) g_rs = make_rsrc(p.g + (int64_t)start * p.g_st + (int64_t)qh * p.g_sh, rows_bytes(L, p.g_st, D));
     const int q_row = (int)p.q_st * 2, k_row = (int)p.k_st * 2, v_row = (int)p.v_st * 2;
 
-    // Key range [klo, klo + ntiles * BN) of query tile qt: the union of its rows' windows
-    // (never empty for a tile inside the segment: each row sees at least itself).
+    // Key range [klo, klo + ntiles * BN) of query tile qt: the union of its rows' windows, in
+    // key positions (at least one tile: rows that reach no key come out as zero).
     auto key_range = [&](int qt, int &klo, int &ntiles) {
-        const int q0 = qt * BM, rows_end = min(L, q0 + BM);
+        const int q0 = qt * BM + off, rows_end = min(L, qt * BM + BM) + off;
         klo = wl >= 0 ? max(0, q0 - wl) : 0;
-        const int khi = wr >= 0 ? min(L, rows_end + wr) : L;
+        const int khi = wr >= 0 ? min(Lk, rows_end + wr) : Lk;
         ntiles = max(1, (khi - klo + BN - 1) / BN);
     };
 
@@ -279,6 +282,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
         const int myrow = r0 + col;
         const bool wave_active = r0 < L;
         const int wr1 = min(L, r0 + 32);
+        const int a0 = r0 + off, a1 = wr1 + off, arow = myrow + off;  // in key positions
 
         // Q steps: lanes whose row is in step i's part read their fragments; the empty asm
         // ends the reads' scope before the next barrier frees the stage.
@@ -313,13 +317,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
                 const int kt0 = klo + t * BN;
                 // Every block of the tile live and unmasked for all of this wave's rows: the
                 // common case, taken without any per-block test.
-                const bool full = (kt0 + BN <= L) && (wl < 0 || (wr1 - 1) - kt0 <= wl) && (wr < 0 || (kt0 + BN - 1) - r0 <= wr);
+                const bool full = (kt0 + BN <= Lk) && (wl < 0 || (a1 - 1) - kt0 <= wl) && (wr < 0 || (kt0 + BN - 1) - a0 <= wr);
                 // (Kept as a lambda: the register allocator then fits the step in 136-148 VGPRs;
                 // written inline the same code spills.)
                 auto kv_step = [&]() {
                     bool live[NB];
 #pragma unroll
-                    for (int b = 0; b < NB; ++b) live[b] = full || block_live(kt0 + 32 * b, L, r0, wr1, wl, wr);
+                    for (int b = 0; b < NB; ++b) live[b] = full || block_live(kt0 + 32 * b, Lk, a0, a1, wl, wr);
                     f32x16 s[NB];
                     bf16x8 pb[NB][2];
                     float st[4];
@@ -343,8 +347,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
                             for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
 #pragma unroll
                             for (int c = 0; c < DC; ++c) acc = mfma32(ld_s16(kt + 32 * b * D + kbase_c[c]), qf[c], acc);
-                            if (!full && !block_full(kb0, L, r0, wr1, wl, wr)) {
-                                const uint32_t km = key_mask(kb0, kg, myrow, L, wl, wr);
+                            if (!full && !block_full(kb0, Lk, a0, a1, wl, wr)) {
+                                const uint32_t km = key_mask(kb0, kg, arow, Lk, wl, wr);
 #pragma unroll
                                 for (int j = 0; j < 16; ++j) acc[j] = mask_score(acc[j], km, acc_key(j, 0));
                             }

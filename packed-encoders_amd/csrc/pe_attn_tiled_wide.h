@@ -38,10 +38,13 @@ __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
     const int seg = w.x, qt_first = w.y;
     if (seg < 0 || seg >= p.n_seq || qt_first < 0 || p.strip < 1) return;  // a plan made for other arguments
     const int start = p.cu[seg];
-    const int L = p.cu[seg + 1] - start;
+    const int L = p.cu[seg + 1] - start;  // query rows
+    const int kstart = p.cuk[seg];
+    const int Lk = p.cuk[seg + 1] - kstart;  // keys
     // A segment longer than the caller's max_seqlen breaks the contract the host sized the
     // 32-bit buffer offsets by: its rows are left unwritten rather than addressed.
-    if (L > p.max_seqlen) return;
+    if (L > p.max_seqlen || Lk > p.max_seqlen_k || Lk < 0) return;
+    const int off = Lk - L;  // key position of query row 0 (queries end-aligned to their keys)
     const int nq = (L + BM - 1) / BM;
     if (qt_first >= nq) return;
     const int qt_end = min(nq, qt_first + p.strip);
@@ -56,8 +59,8 @@ __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
     const int wl = WIN ? p.wl : -1, wr = WIN ? p.wr : -1;
 
     const __amdgpu_buffer_rsrc_t q_rs = make_rsrc(p.q + (int64_t)start * p.q_st + (int64_t)qh * p.q_sh, rows_bytes(L, p.q_st, D));
-    const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(p.k + (int64_t)start * p.k_st + (int64_t)kvh * p.k_sh, rows_bytes(L, p.k_st, D));
-    const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(p.v + (int64_t)start * p.v_st + (int64_t)kvh * p.v_sh, rows_bytes(L, p.v_st, D));
+    const __amdgpu_buffer_rsrc_t k_rs = make_rsrc(p.k + (int64_t)kstart * p.k_st + (int64_t)kvh * p.k_sh, rows_bytes(Lk, p.k_st, D));
+    const __amdgpu_buffer_rsrc_t v_rs = make_rsrc(p.v + (int64_t)kstart * p.v_st + (int64_t)kvh * p.v_sh, rows_bytes(Lk, p.v_st, D));
     const __amdgpu_buffer_rsrc_t o_rs = make_rsrc(p.o + (int64_t)start * p.o_st + (int64_t)qh * p.o_sh, rows_bytes(L, p.o_st, D));
     __amdgpu_buffer_rsrc_t g_rs = o_rs;
     if constexpr (GATE) g_rs = make_rsrc(p.g + (int64_t)start * p.g_st + (int64_t)qh * p.g_sh, rows_bytes(L, p.g_st, D));
@@ -66,9 +69,9 @@ __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
     // Key range [klo, klo + ntiles * BN) of query tile qt: the union of its rows' windows
     // (never empty for a tile inside the segment: each row sees at least itself).
     auto key_range = [&](int qt, int &klo, int &ntiles) {
-        const int q0 = qt * BM, rows_end = min(L, q0 + BM);
+        const int q0 = qt * BM + off, rows_end = min(L, qt * BM + BM) + off;  // key positions
         klo = wl >= 0 ? max(0, q0 - wl) : 0;
-        const int khi = wr >= 0 ? min(L, rows_end + wr) : L;
+        const int khi = wr >= 0 ? min(Lk, rows_end + wr) : Lk;
         ntiles = max(1, (khi - klo + BN - 1) / BN);
     };
 
@@ -245,15 +248,15 @@ __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const int kb0 = kt0 + 32 * b;
-                live[b] = block_live(kb0, L, r0, wr1, wl, wr);
+                live[b] = block_live(kb0, Lk, r0 + off, wr1 + off, wl, wr);
                 if (live[b]) {
                     f32x16 acc;
 #pragma unroll
                     for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
 #pragma unroll
                     for (int c = 0; c < DC; ++c) acc = mfma32(ld_s16(kt + 32 * b * D + kbase_c[c]), qf[c], acc);
-                    if (!block_full(kb0, L, r0, wr1, wl, wr)) {
-                        const uint32_t km = key_mask(kb0, kg, myrow, L, wl, wr);
+                    if (!block_full(kb0, Lk, r0 + off, wr1 + off, wl, wr)) {
+                        const uint32_t km = key_mask(kb0, kg, myrow + off, Lk, wl, wr);
 #pragma unroll
                         for (int j = 0; j < 16; ++j) acc[j] = mask_score(acc[j], km, acc_key(j, 0));
                     }

@@ -39,7 +39,8 @@ def _aligned(t: Tensor) -> Tensor:
 
 def _args(q: Tensor, k: Tensor, v: Tensor, o: Tensor, cu: Tensor, max_seqlen: int, scale: float,
           window_left: int, window_right: int, causal: bool, gate: Tensor | None,
-          short_max: int, strip: int = 0) -> _lib.AttnArgs:
+          short_max: int, strip: int = 0, cu_k: Tensor | None = None,
+          max_seqlen_k: int = 0) -> _lib.AttnArgs:
     a = _lib.AttnArgs()
     a.struct_size = ctypes.sizeof(_lib.AttnArgs)
     a.dtype = _lib.DTYPE_BF16
@@ -61,14 +62,25 @@ def _args(q: Tensor, k: Tensor, v: Tensor, o: Tensor, cu: Tensor, max_seqlen: in
     a.causal = 1 if causal else 0
     a.short_max = int(short_max)
     a.strip = int(strip)
+    if cu_k is not None:
+        a.cu_seqlens_k = cu_k.data_ptr()
+        a.total_tokens_k = k.shape[0]
+        a.max_seqlen_k = int(max_seqlen_k)
     return a
 
 
-def _check_tensors(q: Tensor, k: Tensor, v: Tensor, cu: Tensor, gate: Tensor | None) -> None:
+def _check_tensors(q: Tensor, k: Tensor, v: Tensor, cu: Tensor, gate: Tensor | None,
+                   cu_k: Tensor | None = None) -> None:
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
         raise ValueError("varlen attention expects [tokens, heads, head_dim] q/k/v")
-    if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+    same_rows = cu_k is not None or q.shape[0] == k.shape[0]
+    if k.shape != v.shape or not same_rows or q.shape[2] != k.shape[2]:
         raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
+    if cu_k is not None:
+        if cu_k.dtype != torch.int32 or cu_k.ndim != 1 or cu_k.numel() != cu.numel():
+            raise ValueError("cu_seqlens_k must be a 1-D int32 tensor with cu_seqlens' length")
+        if cu_k.device != q.device:
+            raise ValueError("cu_seqlens_k must be on q's device")
     if q.shape[1] % k.shape[1]:
         raise ValueError("query heads must be a multiple of kv heads")
     if q.dtype != _BF16 or k.dtype != _BF16 or v.dtype != _BF16:
@@ -102,16 +114,18 @@ def shared_plans():
         _PLANS.reset(token)
 
 
-def _plan_key(args: _lib.AttnArgs, cu: Tensor) -> tuple:
+def _plan_key(args: _lib.AttnArgs, cu: Tensor, cu_k: Tensor | None = None) -> tuple:
+    kv = (None,) if cu_k is None else (id(cu_k), cu_k.data_ptr(), args.total_tokens_k, args.max_seqlen_k)
     return (id(cu), cu.data_ptr(), cu.numel(), args.total_tokens, args.max_seqlen, args.n_heads_q,
             args.n_heads_kv, args.head_dim, args.window_left, args.window_right, args.causal, args.short_max,
-            args.strip)
+            args.strip, *kv)
 
 
 def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int,
                  softmax_scale: float, window_left: int, window_right: int, causal: bool,
-                 gate: Tensor | None, short_max: int) -> Tensor:
-    _check_tensors(q, k, v, cu_seqlens, gate)
+                 gate: Tensor | None, short_max: int, cu_seqlens_k: Tensor | None = None,
+                 max_seqlen_k: int = 0) -> Tensor:
+    _check_tensors(q, k, v, cu_seqlens, gate, cu_seqlens_k)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     gate = _aligned(gate) if gate is not None else None
     out = torch.empty(q.shape, dtype=_BF16, device=q.device)
@@ -119,7 +133,7 @@ def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen
         return out
     lib = _lib.library()
     args = _args(q, k, v, out, cu_seqlens, max_seqlen, softmax_scale, window_left, window_right,
-                 causal, gate, short_max)
+                 causal, gate, short_max, cu_k=cu_seqlens_k, max_seqlen_k=max_seqlen_k)
     stream = torch.cuda.current_stream(q.device).cuda_stream
     plans = _PLANS.get()
     if plans is None:
@@ -130,7 +144,7 @@ def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen
                                         size.value, stream)
         _lib.check(status, "pe_varlen_attn_fwd")
         return out
-    key = _plan_key(args, cu_seqlens)
+    key = _plan_key(args, cu_seqlens, cu_seqlens_k)
     entry = plans.get(key)
     if entry is None:
         size = ctypes.c_size_t(0)
@@ -138,7 +152,7 @@ def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen
         workspace = torch.empty(size.value, dtype=torch.uint8, device=q.device) if size.value else None
         ptr = workspace.data_ptr() if workspace is not None else None
         _lib.check(lib.pe_attn_plan(ctypes.byref(args), ptr, size.value, stream), "pe_attn_plan")
-        entry = plans[key] = (cu_seqlens, workspace, size.value)
+        entry = plans[key] = ((cu_seqlens, cu_seqlens_k), workspace, size.value)
     _, workspace, nbytes = entry
     ptr = workspace.data_ptr() if workspace is not None else None
     _lib.check(lib.pe_attn_short_fwd(ctypes.byref(args), stream), "pe_attn_short_fwd")
@@ -159,6 +173,13 @@ def _short_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen:
     stream = torch.cuda.current_stream(q.device).cuda_stream
     _lib.check(lib.pe_packed_short_attn_fwd(ctypes.byref(args), stream), "pe_packed_short_attn_fwd")
     return out
+
+
+def _varlen_kv_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens_q: Tensor, cu_seqlens_k: Tensor,
+                    max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float, window_left: int,
+                    window_right: int, causal: bool, gate: Tensor | None, short_max: int) -> Tensor:
+    return _varlen_impl(q, k, v, cu_seqlens_q, max_seqlen_q, softmax_scale, window_left, window_right, causal,
+                        gate, short_max, cu_seqlens_k, max_seqlen_k)
 
 
 def _meta(q: Tensor, *args, **kwargs) -> Tensor:
@@ -215,12 +236,17 @@ def _register() -> None:
         lib.define("packed_short_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, int max_seqlen, "
                    "float softmax_scale, int window_left, int window_right) -> Tensor")
         lib.define("rope_qkv(Tensor qkv, Tensor cos, Tensor sin, int h, int d) -> Tensor[]")
+        lib.define("varlen_attention_kv(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
+                   "int max_seqlen_q, int max_seqlen_k, float softmax_scale, int window_left, int window_right, "
+                   "bool causal, Tensor? gate, int short_max) -> Tensor")
     except RuntimeError:
         return  # already defined by an earlier import in this process
     lib.impl("varlen_attention", _varlen_impl, "CUDA")
     lib.impl("varlen_attention", _meta, "Meta")
     lib.impl("packed_short_attention", _short_impl, "CUDA")
     lib.impl("packed_short_attention", _meta, "Meta")
+    lib.impl("varlen_attention_kv", _varlen_kv_impl, "CUDA")
+    lib.impl("varlen_attention_kv", _meta, "Meta")
     lib.impl("rope_qkv", _rope_impl, "CUDA")
     lib.impl("rope_qkv", _rope_meta, "Meta")
     globals()["_TORCH_LIBRARY"] = lib
@@ -232,7 +258,8 @@ _register()
 def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int, *,
                      softmax_scale: float | None = None, window: tuple[int, int] = (-1, -1),
                      causal: bool = False, gate: Tensor | None = None,
-                     short_max: int | None = None) -> Tensor:
+                     short_max: int | None = None, cu_seqlens_k: Tensor | None = None,
+                     max_seqlen_k: int | None = None) -> Tensor:
     """Packed varlen attention: q ``[T, Hq, D]``, k/v ``[T, Hkv, D]`` bf16, int32 ``cu_seqlens``.
 
     ``window=(left, right)`` bounds ``i - j <= left`` and ``j - i <= right`` (-1 unbounded,
@@ -241,12 +268,24 @@ def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_se
     segments of at most that length to the LDS-resident short kernel (None: the gfx950 policy
     default). Returns a new contiguous ``[T, Hq, D]``; rows beyond ``cu_seqlens[-1]`` are not
     written. Forward only.
+
+    ``cu_seqlens_k`` / ``max_seqlen_k`` give k/v ``[Tk, Hkv, D]`` segments of their own
+    (FlashAttention's varlen form): query segment s is the tail of key segment s, its row r at
+    key position ``r + Lk - Lq``, which ``causal`` and ``window`` are measured from (the
+    reference's prefixed form, packed_encoders/runtime/attention.py:15-19,236-245). A row that
+    reaches no key comes out as zero.
     """
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
         raise ValueError("the HIP packed attention is forward-only; call it under torch.no_grad()")
     scale = q.shape[-1] ** -0.5 if softmax_scale is None else float(softmax_scale)
     if short_max is None:
         short_max = -1
+    if cu_seqlens_k is not None:
+        if max_seqlen_k is None:
+            raise ValueError("cu_seqlens_k needs max_seqlen_k")
+        return torch.ops.pe_hip.varlen_attention_kv(q, k, v, cu_seqlens, cu_seqlens_k, int(max_seqlen),
+                                                    int(max_seqlen_k), scale, int(window[0]), int(window[1]),
+                                                    bool(causal), gate, int(short_max))
     return torch.ops.pe_hip.varlen_attention(q, k, v, cu_seqlens, int(max_seqlen), scale,
                                              int(window[0]), int(window[1]), bool(causal), gate,
                                              int(short_max))

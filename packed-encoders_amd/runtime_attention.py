@@ -13,8 +13,8 @@ segment and grouped KV heads, in both layouts the engines use:
 Candidates, in order: ``"hip"`` (this library's kernels: packed and padded forms are one varlen
 call each, GQA, causal and window handled in-kernel) and ``"sdpa"`` (always passes, so
 selection never fails). A causal engine also gets the *prefixed* form, where a query segment is
-the tail of a longer key segment (mask aligned to the segment end); the HIP kernels take equal
-query and key segments, so that form is SDPA's. Rejections keep their reason.
+the tail of a longer key segment (mask aligned to the segment end): one varlen call with
+separate key segments (``cu_seqlens_k``). Rejections keep their reason.
 """
 
 from __future__ import annotations
@@ -79,8 +79,10 @@ def _hip(window, scale) -> tuple[Callable, ...]:
         return varlen_attention(q, k, v, static.seg_cu32, static.seq, softmax_scale=scale, window=window,
                                 causal=causal)
 
-    def prefixed(*args, **kwargs):
-        raise NotImplementedError("the HIP kernels take equal query and key segments")
+    def prefixed(q, k, v, cu_q, cu_k, max_q, max_k, lengths_q, lengths_k, causal):
+        # query segment s is the tail of key segment s: the kernels' separate key segments
+        return varlen_attention(q, k, v, cu_q, max_q, softmax_scale=scale, window=window, causal=causal,
+                                cu_seqlens_k=cu_k, max_seqlen_k=max_k)
 
     return packed, padded, prefixed
 

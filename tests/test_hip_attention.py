@@ -57,8 +57,11 @@ def _assert_parity(got, want, cu, *, max_abs=MAX_ABS, min_cos=MIN_COS):
     assert np.isfinite(g).all()
     err = np.abs(g - w)
     assert err.max() <= max_abs, f"max abs {err.max():.4g}"
-    cos = oa.cosine_per_token(g, w)
-    assert cos.min() >= min_cos, f"min cosine {cos.min():.6f}"
+    # rows that reach no key (separate key segments) are exactly zero in both; cosine elsewhere
+    zero = ~np.any(w.reshape(w.shape[0], -1), axis=1)
+    assert not np.any(g.reshape(g.shape[0], -1)[zero]), "rows that reach no key must be zero"
+    cos = oa.cosine_per_token(g[~zero], w[~zero])
+    assert cos.size == 0 or cos.min() >= min_cos, f"min cosine {cos.min():.6f}"
     return float(err.max()), float(err.mean())
 
 
@@ -349,6 +352,37 @@ def test_window_gate_and_short_routing(pe, window, causal):
     got = _launch(_lib.library(), qd, kd, vd, cud, max(lengths), window, causal, gate=gd, short_max=64)
     want = _oracle(q, k, v, cu, scale=0.125, window=window, causal=causal, gate=gt)
     _assert_parity(got, want, cu)
+
+
+PREFIX_Q = [5, 1, 37, 16, 130, 300, 64, 20, 0, 7, 260]
+PREFIX_K = [40, 64, 37, 80, 700, 300, 200, 5, 50, 7, 1000]  # the reference's probe pairs, then longer
+
+
+@pytest.mark.parametrize("short_max", [0, 64])
+@pytest.mark.parametrize("d,hq,hkv", [(64, 4, 4), (64, 6, 2), (128, 4, 2), (256, 8, 2)])
+@pytest.mark.parametrize("window,causal", [((-1, -1), True), ((-1, -1), False), ((48, -1), True), ((20, 9), False)],
+                         ids=["causal", "bidir", "causal-window", "window"])
+def test_separate_key_segments_match_oracle(pe, window, causal, d, hq, hkv, short_max):
+    """Query segments that are the tails of longer (or equal, or shorter) key segments
+    (FlashAttention's cu_seqlens_k; the reference's prefixed form): causal bound and window
+    measured from each query's key position, every kernel (short, tiled, wide), GQA. The
+    reference's own probe pairs come first; a 20-query segment over 5 keys leaves its first
+    causal rows with no key (zeros), and empty query or key segments are included."""
+    announce(f"separate key segments window={window} causal={causal} d={d} heads={hq}/{hkv} short_max={short_max}")
+    g = torch.Generator().manual_seed(67)
+    q = torch.randn(sum(PREFIX_Q), hq, d, generator=g).bfloat16()
+    k = torch.randn(sum(PREFIX_K), hkv, d, generator=g).bfloat16()
+    v = torch.randn(sum(PREFIX_K), hkv, d, generator=g).bfloat16()
+    cu_q = torch.tensor([0, *np.cumsum(PREFIX_Q).tolist()], dtype=torch.int32)
+    cu_k = torch.tensor([0, *np.cumsum(PREFIX_K).tolist()], dtype=torch.int32)
+    qd, kd, vd, cqd, ckd = _dev(q, k, v, cu_q, cu_k)
+    with torch.inference_mode():
+        got = pe.varlen_attention(qd, kd, vd, cqd, max(PREFIX_Q), softmax_scale=0.125, window=window, causal=causal,
+                                  short_max=short_max, cu_seqlens_k=ckd, max_seqlen_k=max(PREFIX_K))
+    f = lambda t: t.float().numpy()
+    want = oa.packed_attention(f(q), f(k), f(v), cu_q.numpy(), scale=0.125, window=window, causal=causal,
+                               cu_seqlens_k=cu_k.numpy())
+    _assert_parity(got, want, cu_q)
 
 
 @pytest.mark.parametrize("jump", [4.0, 10.0], ids=["below-guard", "past-guard"])

@@ -156,7 +156,12 @@ def test_select_attention_picks_hip_for_gqa_causal_and_windows(pe):
         assert choice.name == "hip", choice.rejected
         assert choice.max_abs_err < 2e-2
         if kw["causal"]:
-            assert choice.prefixed_name == "sdpa" and "hip:prefixed" in choice.rejected
+            # the prefixed form (queries the tail of longer key segments) runs the HIP kernels too
+            assert choice.prefixed_name == "hip", choice.rejected
+            assert choice.prefixed_max_abs_err < 2e-2
+    choice = pe.select_attention(device=torch.device("cuda"), n_heads=8, n_kv_heads=2, head_dim=64, causal=True,
+                                 window=(32, -1), bidirectional_prefixed=True)
+    assert choice.name == "hip" and choice.prefixed_name == "hip", choice.rejected
 
 
 def test_modernbert_base_shape_packed_forward(pe):

@@ -48,6 +48,50 @@ def test_vectorised_oracle_matches_brute_force(window, causal):
     np.testing.assert_allclose(fast, slow, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("window,causal", [((-1, -1), False), ((-1, -1), True), ((4, 2), False), ((3, -1), True),
+                                           ((0, 0), False)])
+def test_prefixed_oracle_matches_brute_force(window, causal):
+    """Separate key segments: the vectorised oracle against the scalar loop, on short tails, a
+    single query, a square pair and a long prefix, plus an empty query segment and an empty key
+    segment (its queries reach nothing: zeros)."""
+    rng = np.random.default_rng(11)
+    lq, lk = [2, 1, 3, 4, 0, 2], [5, 4, 3, 9, 2, 0]
+    q = _rand(rng, sum(lq), 2, 4)
+    k, v = _rand(rng, sum(lk), 1, 4), _rand(rng, sum(lk), 1, 4)
+    got = oa.packed_attention(q, k, v, _cu(lq), scale=0.5, window=window, causal=causal, cu_seqlens_k=_cu(lk))
+    want = oa.brute_force_attention(q, k, v, _cu(lq), scale=0.5, window=window, causal=causal, cu_seqlens_k=_cu(lk))
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    assert np.all(got[-2:] == 0.0)  # the last query segment has no keys
+
+
+@pytest.mark.parametrize("window,causal", [((-1, -1), False), ((-1, -1), True), ((6, 3), False), ((9, -1), True)])
+def test_prefixed_queries_are_the_tail_of_full_attention(window, causal):
+    """A query segment aligned to the end of its key segment reads exactly what the last rows
+    of self-attention over the whole key segment read: giving the full segment queries whose
+    tail is the prefixed queries, the full result's tail must equal the prefixed result. An
+    alignment to the segment start, or an off-by-one shift, breaks this."""
+    rng = np.random.default_rng(12)
+    lq, lk = [3, 1, 20, 11], [17, 9, 20, 40]
+    hq, hkv, d = 4, 2, 8
+    kk, vv = _rand(rng, sum(lk), hkv, d), _rand(rng, sum(lk), hkv, d)
+    q_full = _rand(rng, sum(lk), hq, d)
+    cuk = _cu(lk)
+    tails = np.concatenate([np.arange(cuk[i + 1] - n, cuk[i + 1]) for i, n in enumerate(lq)])
+    prefixed = oa.packed_attention(q_full[tails], kk, vv, _cu(lq), scale=0.3, window=window, causal=causal,
+                                   cu_seqlens_k=cuk)
+    full = oa.packed_attention(q_full, kk, vv, cuk, scale=0.3, window=window, causal=causal)
+    np.testing.assert_allclose(prefixed, full[tails], rtol=1e-12, atol=1e-12)
+
+
+def test_prefixed_with_equal_segments_is_self_attention():
+    rng = np.random.default_rng(13)
+    lengths = [4, 9, 1]
+    q, k, v = _rand(rng, 14, 2, 8), _rand(rng, 14, 2, 8), _rand(rng, 14, 2, 8)
+    a = oa.packed_attention(q, k, v, _cu(lengths), scale=0.4, window=(2, 1), cu_seqlens_k=_cu(lengths))
+    b = oa.packed_attention(q, k, v, _cu(lengths), scale=0.4, window=(2, 1))
+    assert np.array_equal(a, b)
+
+
 def test_single_token_segments_return_v():
     rng = np.random.default_rng(2)
     q, k, v = _rand(rng, 6, 3, 16), _rand(rng, 6, 3, 16), _rand(rng, 6, 3, 16)
