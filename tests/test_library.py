@@ -114,6 +114,23 @@ def test_bad_arguments_are_rejected_before_any_launch(lib, field, value, status)
     assert lib.pe_varlen_attn_fwd(ctypes.byref(a), None, 0, None) == status
 
 
+def test_key_segment_sizes_are_checked_and_size_the_workspace(lib):
+    """With cu_seqlens_k given, negative key sizes are rejected; a batch whose query segments
+    are all short still needs the tiled workspace when its key segments are long, and that
+    workspace counts every segment as possibly long."""
+    a = _args(max_seqlen=64)
+    a.cu_seqlens_k = 8  # any non-NULL value: only sizes are read here
+    a.total_tokens_k, a.max_seqlen_k = -1, 100
+    rc, _ = _ws(lib, a)
+    assert rc == -1
+    a.total_tokens_k, a.max_seqlen_k = 5000, 300
+    rc, size = _ws(lib, a)
+    n = a.n_seq
+    assert rc == 0 and size == 256 + 8 * min(n * 1, (a.total_tokens + n * 127) // 128)
+    rc, size = _ws(lib, _args(max_seqlen=64))  # same queries, keys shared: no tiled work
+    assert rc == 0 and size == 0
+
+
 def test_missing_device_pointers_are_rejected(lib):
     a = _args()  # q/k/v/o/cu are NULL with work to do
     assert lib.pe_varlen_attn_fwd(ctypes.byref(a), None, 0, None) == -1
