@@ -197,8 +197,9 @@ int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
     p.hgroups = p.hq / G;
     // Banded head_dim 64 launches deal work to the 8 XCDs in runs (tiled_attn_kernel): whole
     // rounds of runs, the surplus workgroups exiting at once.
-    const int64_t run = 8LL * pe::kXcdRun * p.hgroups;
-    const int64_t blocks = (D == 64 && WIN) ? (cap * p.hgroups + run - 1) / run * run : cap * p.hgroups;
+    // head_dim 128 / 256 launches deal every call that way, in runs of wide_run() workgroups.
+    const int64_t run = D == 64 ? 8LL * pe::kXcdRun * p.hgroups : 8LL * pe::wide_run<D>(p.hgroups);
+    const int64_t blocks = (D > 64 || WIN) ? (cap * p.hgroups + run - 1) / run * run : cap * p.hgroups;
     if (blocks <= 0) return PE_ATTN_OK;
     if (blocks > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
     if constexpr (D == 64)
@@ -307,7 +308,7 @@ int pe_attn_plan(const pe_attn_args *a, void *workspace, size_t workspace_bytes,
     const int wr = a->causal ? 0 : a->window_right;
     hipLaunchKernelGGL(pe::plan_kernel, dim3(1), dim3(1024), 0, stream, a->cu_seqlens,
                        a->cu_seqlens_k ? a->cu_seqlens_k : a->cu_seqlens, a->n_seq, plan.sm, plan.bm, plan.strip,
-                       a->window_left, wr, work, count, (int)plan.cap);
+                       a->window_left, wr, a->head_dim > 64 ? 1 : 0, work, count, (int)plan.cap);
     return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
 }
 

@@ -195,4 +195,50 @@ __device__ __forceinline__ bf16x4 out4(float a0, float a1, float a2, float a3, b
     return r;
 }
 
+// Epilogue of a wave's query block: lane (col, kg) holds row `col` of O^T in o[db][4 jj + i] =
+// dims 32 db + 8 jj + 4 kg + i, unnormalised. Scales by inv, applies the optional gate and
+// stores 8 bytes per (db, jj). Gate loads go out in batches of 8 (two 32-dim blocks), two
+// batches in flight: batch b + 1 is waited for after batch b's stores are issued (so the wait
+// does not include them) and batch b + 2 is issued next, into b's registers. Only the first
+// batch's latency is exposed; a load next to each use would wait once per 8-byte chunk, and
+// each such wait would also cover every store before it.
+template <int DB, bool GATE>
+__device__ __forceinline__ void store_block(const f32x16 (&o)[DB], float inv, int kg, __amdgpu_buffer_rsrc_t o_rs,
+                                            int ooff, __amdgpu_buffer_rsrc_t g_rs, int goff) {
+    auto chunk = [&](int db, int jj, bf16x4 g4) {
+        const int d0 = db * 32 + 8 * jj + 4 * kg;
+        buf_st8(o_rs, ooff + d0 * 2,
+                out4<GATE>(o[db][4 * jj] * inv, o[db][4 * jj + 1] * inv, o[db][4 * jj + 2] * inv,
+                           o[db][4 * jj + 3] * inv, g4));
+    };
+    if constexpr (!GATE) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) chunk(db, jj, bf16x4{});
+    } else {
+        static_assert(DB % 2 == 0, "gate batches are two 32-dim blocks");
+        constexpr int NBATCH = DB / 2;
+        bf16x4 g[2][8];
+        auto load = [&](int b, bf16x4 (&gb)[8]) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) gb[c] = buf_ld8(g_rs, goff + ((2 * b + c / 4) * 32 + 8 * (c % 4) + 4 * kg) * 2, 0);
+        };
+        auto force = [&](bf16x4 (&gb)[8]) {
+            asm volatile("" : "+v"(gb[0]), "+v"(gb[1]), "+v"(gb[2]), "+v"(gb[3]), "+v"(gb[4]), "+v"(gb[5]),
+                         "+v"(gb[6]), "+v"(gb[7]));
+        };
+        load(0, g[0]);
+        if (NBATCH > 1) load(1, g[1]);
+        force(g[0]);
+#pragma unroll
+        for (int b = 0; b < NBATCH; ++b) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) chunk(2 * b + c / 4, c % 4, g[b & 1][c]);
+            if (b + 1 < NBATCH) force(g[(b + 1) & 1]);
+            if (b + 2 < NBATCH) load(b + 2, g[b & 1]);
+        }
+    }
+}
+
 }  // namespace pe

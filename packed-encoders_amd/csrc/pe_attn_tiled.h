@@ -432,17 +432,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
             const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
             const int ooff = myrow * (int)p.o_st * 2;
             const int goff = GATE ? myrow * (int)p.g_st * 2 : 0;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const int d0 = db * 32 + 8 * jj + 4 * kg;
-                    bf16x4 g4 = {};
-                    if constexpr (GATE) g4 = buf_ld8(g_rs, goff + d0 * 2, 0);
-                    buf_st8(o_rs, ooff + d0 * 2,
-                            out4<GATE>(o[db][4 * jj] * inv, o[db][4 * jj + 1] * inv, o[db][4 * jj + 2] * inv,
-                                       o[db][4 * jj + 3] * inv, g4));
-                }
+            store_block<DB, GATE>(o, inv, kg, o_rs, ooff, g_rs, goff);
         }
     }
     // Loads of void steps may still be landing in LDS: drain before the workgroup ends.

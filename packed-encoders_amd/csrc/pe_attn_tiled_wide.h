@@ -12,6 +12,15 @@
 
 namespace pe {
 
+// Workgroups per run that one XCD takes in a row: as many as its 32 CUs hold at once (one
+// workgroup per CU for head_dim 256, two for 128), in whole work entries (all head groups of
+// each). The launch rounds the grid up to whole rounds of 8 runs.
+template <int D>
+__host__ __device__ inline int wide_run(int hgroups) {
+    constexpr int kResident = D >= 256 ? 32 : 64;
+    return hgroups * (hgroups < kResident ? kResident / hgroups : 1);
+}
+
 template <int D, int G, int BN, int NS, bool GATE, bool WIN>
 __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
     static_assert(D % 32 == 0 && BN % 32 == 0 && (4 % G) == 0 && NS >= 2, "tile shape");
@@ -31,8 +40,15 @@ __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
 
     __shared__ __attribute__((aligned(16))) __bf16 ring[NS][2][TILE];
 
-    const int entry = blockIdx.x / p.hgroups;
-    const int hg = blockIdx.x - entry * p.hgroups;
+    // Work item: the plan lists each segment's query tiles contiguously; workgroup i runs on
+    // XCD i % 8, and the runs of wide_run() consecutive items are dealt to the XCDs in turn,
+    // so the tiles of a segment run side by side on one XCD and re-read its keys from that
+    // XCD's L2 (dealt one item per XCD, every tile fetched them again from memory).
+    const int rh = wide_run<D>(p.hgroups);
+    const int j = (int)(blockIdx.x >> 3);
+    const int item = ((j / rh) * 8 + (int)(blockIdx.x & 7)) * rh + j % rh;
+    const int entry = item / p.hgroups;
+    const int hg = item - entry * p.hgroups;
     if (entry >= *p.work_count) return;
     const int2 w = p.work[entry];
     const int seg = w.x, qt_first = w.y;
@@ -312,17 +328,7 @@ __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
                 const int ooff = myrow * (int)p.o_st * 2;
                 const int goff = GATE ? myrow * (int)p.g_st * 2 : 0;
-#pragma unroll
-                for (int db = 0; db < DB; ++db)
-#pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const int d0 = db * 32 + 8 * jj + 4 * kg;
-                        bf16x4 g4 = {};
-                        if constexpr (GATE) g4 = buf_ld8(g_rs, goff + d0 * 2, 0);
-                        buf_st8(o_rs, ooff + d0 * 2,
-                                out4<GATE>(o[db][4 * jj] * inv, o[db][4 * jj + 1] * inv, o[db][4 * jj + 2] * inv,
-                                           o[db][4 * jj + 3] * inv, g4));
-                    }
+                store_block<DB, GATE>(o, inv, kg, o_rs, ooff, g_rs, goff);
             }
             reset();
             if (qt + 1 >= qt_end) break;
