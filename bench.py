@@ -121,10 +121,13 @@ def kernel_instance(stage, workload, layer, short_max):
         return f"pe::short_attn_kernel<{d}, {sk}, {hpw}, {str(layer.gate).lower()}>"
     g = math.gcd(workload.n_heads_q // workload.n_heads_kv, 4)
     bn = 32 if d >= 256 else 64
-    ns = 3 if d == 64 else (4 if d == 256 else 2)
+    ns = 3 if d == 64 else 2
     win = layer.window != (-1, -1) or layer.causal
+    flags = f"{str(layer.gate).lower()}, {str(win).lower()}"
+    if d == 256:
+        return f"pe::wide16_attn_kernel<{d}, 4, {g}, {ns}, {flags}>"  # four waves per workgroup
     name = "tiled_attn_kernel" if d == 64 else "wide_attn_kernel"
-    return f"pe::{name}<{d}, {g}, {bn}, {ns}, {str(layer.gate).lower()}, {str(win).lower()}>"
+    return f"pe::{name}<{d}, {g}, {bn}, {ns}, {flags}>"
 
 
 def gpu_bench(args, workload):

@@ -14,7 +14,7 @@
 #include "pe_attn_plan.h"
 #include "pe_attn_short.h"
 #include "pe_attn_tiled.h"
-#include "pe_attn_tiled_wide.h"
+#include "pe_attn_tiled_wide16.h"
 #include "pe_rope.h"
 
 namespace {
@@ -182,14 +182,22 @@ int launch_short(const AttnParams &p, int d, bool gate, int short_max, hipStream
     return PE_ATTN_EUNSUPPORTED;
 }
 
+// head_dim 256 runs wide16_attn_kernel with kWide16Waves waves of 16 query rows per workgroup:
+// four waves (one per SIMD) and a 64 KB ring, so two workgroups share a CU and run out of
+// step (one's softmax and epilogue under the other's MFMAs); eight waves with a 128 KB ring,
+// one workgroup per CU, measured 6% slower on C5.
+constexpr int kWide16Waves = 4;
+
 // Key tile and LDS ring depth per head dim: 48 KB (head_dim 64: three workgroups per CU, two
-// tiles in flight each), 64 KB (head_dim 128: two workgroups per CU) or 128 KB (head_dim 256,
-// whose registers allow one workgroup per CU: four stages, three tiles in flight).
+// tiles in flight each), 64 KB (head_dim 128 and 256: two workgroups per CU).
 template <int D>
 struct TiledShape {
     static constexpr int BN = D >= 256 ? 32 : 64;
-    static constexpr int NS = D == 64 ? 3 : (D == 256 ? 4 : 2);
+    static constexpr int NS = D == 64 ? 3 : (D == 256 ? (kWide16Waves == 8 ? 4 : 2) : 2);
 };
+
+// Query rows per tiled-kernel tile for g query heads per workgroup (the plan's tile height).
+int tile_rows(int head_dim, int g) { return head_dim == 256 ? 16 * kWide16Waves / g : 32 * (4 / g); }
 
 template <int D, int G, bool GATE, bool WIN>
 int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
@@ -197,14 +205,20 @@ int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
     p.hgroups = p.hq / G;
     // Banded head_dim 64 launches deal work to the 8 XCDs in runs (tiled_attn_kernel): whole
     // rounds of runs, the surplus workgroups exiting at once.
-    // head_dim 128 / 256 launches deal every call that way, in runs of wide_run() workgroups.
-    const int64_t run = D == 64 ? 8LL * pe::kXcdRun * p.hgroups : 8LL * pe::wide_run<D>(p.hgroups);
+    // head_dim 128 / 256 launches deal every call that way, in runs of the workgroups an XCD
+    // holds at once.
+    const int64_t run = D == 64    ? 8LL * pe::kXcdRun * p.hgroups
+                        : D == 256 ? 8LL * pe::wide16_run<kWide16Waves, NS>(p.hgroups)
+                                   : 8LL * pe::wide_run(p.hgroups);
     const int64_t blocks = (D > 64 || WIN) ? (cap * p.hgroups + run - 1) / run * run : cap * p.hgroups;
     if (blocks <= 0) return PE_ATTN_OK;
     if (blocks > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
     if constexpr (D == 64)
         hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, NS, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0,
                            stream, p);
+    else if constexpr (D == 256)
+        hipLaunchKernelGGL((pe::wide16_attn_kernel<D, kWide16Waves, G, NS, GATE, WIN>), dim3((unsigned)blocks),
+                           dim3(64 * kWide16Waves), 0, stream, p);
     else
         hipLaunchKernelGGL((pe::wide_attn_kernel<D, G, BN, NS, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0,
                            stream, p);
@@ -245,7 +259,7 @@ int prepare(const pe_attn_args *a, Plan *plan) {
     if (rc) return rc;
     plan->sm = effective_short_max(a);
     plan->g = heads_per_tile(a);
-    plan->bm = 32 * (4 / plan->g);
+    plan->bm = tile_rows(a->head_dim, plan->g);
     plan->strip = effective_strip(a);
     plan->cap = tile_capacity(a, plan->sm, plan->bm, plan->strip);
     if (plan->cap > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
@@ -291,7 +305,7 @@ int pe_attn_workspace_size(const pe_attn_args *a, size_t *bytes) {
     if (rc) return rc;
     const int sm = effective_short_max(a);
     const int g = heads_per_tile(a);
-    const int64_t cap = tile_capacity(a, sm, 32 * (4 / g), effective_strip(a));
+    const int64_t cap = tile_capacity(a, sm, tile_rows(a->head_dim, g), effective_strip(a));
     *bytes = cap > 0 ? kWorkspaceHeader + (size_t)cap * sizeof(int2) : 0;
     return PE_ATTN_OK;
 }

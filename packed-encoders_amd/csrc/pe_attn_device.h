@@ -174,55 +174,57 @@ __device__ __forceinline__ bool block_full(int kb0, int L, int r0, int r1, int w
 
 // Round 4 fp32 outputs to bf16 and apply the optional fused sigmoid gate (g holds the gate's
 // 4 bf16 values): y = bf16(bf16(o) * bf16(sigmoid(g))), the rounding order of the reference's
-// gate kernel (packed_encoders/_kernels/hybrid.py:197-206). The sigmoid's reciprocal is
-// v_rcp_f32 (1 ulp) rather than an IEEE division (about ten instructions): its result is
-// rounded to bf16 next, which a 1-ulp fp32 difference can move by one bf16 step only when the
-// quotient lies within that ulp of a rounding boundary.
+// gate kernel (packed_encoders/_kernels/hybrid.py:197-206). Roundings go two at a time
+// (v_cvt_pk_bf16_f32). The sigmoid's reciprocal is v_rcp_f32 (1 ulp) rather than an IEEE
+// division (about ten instructions): its result is rounded to bf16 next, which a 1-ulp fp32
+// difference can move by one bf16 step only when the quotient lies within that ulp of a
+// rounding boundary.
 template <bool GATE>
 __device__ __forceinline__ bf16x4 out4(float a0, float a1, float a2, float a3, bf16x4 g) {
-    bf16x4 r;
-    r[0] = (__bf16)a0;
-    r[1] = (__bf16)a1;
-    r[2] = (__bf16)a2;
-    r[3] = (__bf16)a3;
-    if constexpr (GATE) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 r01 = __builtin_convertvector(f32x2{a0, a1}, bf16x2);
+    const bf16x2 r23 = __builtin_convertvector(f32x2{a2, a3}, bf16x2);
+    if constexpr (!GATE) {
+        return bf16x4{r01[0], r01[1], r23[0], r23[1]};
+    } else {
+        float sg[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float sg = (float)(__bf16)__builtin_amdgcn_rcpf(1.0f + __expf(-(float)g[i]));
-            r[i] = (__bf16)((float)r[i] * sg);
-        }
+        for (int i = 0; i < 4; ++i) sg[i] = __builtin_amdgcn_rcpf(1.0f + __expf(-(float)g[i]));
+        const bf16x2 s01 = __builtin_convertvector(f32x2{sg[0], sg[1]}, bf16x2);
+        const bf16x2 s23 = __builtin_convertvector(f32x2{sg[2], sg[3]}, bf16x2);
+        const bf16x2 y01 = __builtin_convertvector(
+            __builtin_convertvector(r01, f32x2) * __builtin_convertvector(s01, f32x2), bf16x2);
+        const bf16x2 y23 = __builtin_convertvector(
+            __builtin_convertvector(r23, f32x2) * __builtin_convertvector(s23, f32x2), bf16x2);
+        return bf16x4{y01[0], y01[1], y23[0], y23[1]};
     }
-    return r;
 }
 
-// Epilogue of a wave's query block: lane (col, kg) holds row `col` of O^T in o[db][4 jj + i] =
-// dims 32 db + 8 jj + 4 kg + i, unnormalised. Scales by inv, applies the optional gate and
-// stores 8 bytes per (db, jj). Gate loads go out in batches of 8 (two 32-dim blocks), two
-// batches in flight: batch b + 1 is waited for after batch b's stores are issued (so the wait
-// does not include them) and batch b + 2 is issued next, into b's registers. Only the first
-// batch's latency is exposed; a load next to each use would wait once per 8-byte chunk, and
-// each such wait would also cover every store before it.
-template <int DB, bool GATE>
-__device__ __forceinline__ void store_block(const f32x16 (&o)[DB], float inv, int kg, __amdgpu_buffer_rsrc_t o_rs,
-                                            int ooff, __amdgpu_buffer_rsrc_t g_rs, int goff) {
-    auto chunk = [&](int db, int jj, bf16x4 g4) {
-        const int d0 = db * 32 + 8 * jj + 4 * kg;
-        buf_st8(o_rs, ooff + d0 * 2,
-                out4<GATE>(o[db][4 * jj] * inv, o[db][4 * jj + 1] * inv, o[db][4 * jj + 2] * inv,
-                           o[db][4 * jj + 3] * inv, g4));
+// Epilogue of a wave's query block: NCH chunks of 4 consecutive dims of the lane's query row,
+// chunk c holding vals(c) (unnormalised) for dims dim0(c) .. dim0(c) + 3. Scales by inv,
+// applies the optional gate and stores 8 bytes per chunk. Gate loads go out in batches of 8
+// chunks, two batches in flight: batch b + 1 is waited for after batch b's stores are issued
+// (so the wait does not include them) and batch b + 2 is issued next, into b's registers.
+// Only the first batch's latency is exposed; a load next to each use would wait once per
+// chunk, and each such wait would also cover every store before it.
+template <int NCH, bool GATE, class Vals, class Dim0>
+__device__ __forceinline__ void store_chunks(Vals vals, Dim0 dim0, float inv, __amdgpu_buffer_rsrc_t o_rs, int ooff,
+                                             __amdgpu_buffer_rsrc_t g_rs, int goff) {
+    auto chunk = [&](int c, bf16x4 g4) {
+        const f32x4 v = vals(c);
+        buf_st8(o_rs, ooff + dim0(c) * 2, out4<GATE>(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv, g4));
     };
     if constexpr (!GATE) {
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) chunk(db, jj, bf16x4{});
+        for (int c = 0; c < NCH; ++c) chunk(c, bf16x4{});
     } else {
-        static_assert(DB % 2 == 0, "gate batches are two 32-dim blocks");
-        constexpr int NBATCH = DB / 2;
+        static_assert(NCH % 8 == 0, "gate batches are 8 chunks");
+        constexpr int NBATCH = NCH / 8;
         bf16x4 g[2][8];
         auto load = [&](int b, bf16x4 (&gb)[8]) {
 #pragma unroll
-            for (int c = 0; c < 8; ++c) gb[c] = buf_ld8(g_rs, goff + ((2 * b + c / 4) * 32 + 8 * (c % 4) + 4 * kg) * 2, 0);
+            for (int c = 0; c < 8; ++c) gb[c] = buf_ld8(g_rs, goff + dim0(8 * b + c) * 2, 0);
         };
         auto force = [&](bf16x4 (&gb)[8]) {
             asm volatile("" : "+v"(gb[0]), "+v"(gb[1]), "+v"(gb[2]), "+v"(gb[3]), "+v"(gb[4]), "+v"(gb[5]),
@@ -234,11 +236,24 @@ __device__ __forceinline__ void store_block(const f32x16 (&o)[DB], float inv, in
 #pragma unroll
         for (int b = 0; b < NBATCH; ++b) {
 #pragma unroll
-            for (int c = 0; c < 8; ++c) chunk(2 * b + c / 4, c % 4, g[b & 1][c]);
+            for (int c = 0; c < 8; ++c) chunk(8 * b + c, g[b & 1][c]);
             if (b + 1 < NBATCH) force(g[(b + 1) & 1]);
             if (b + 2 < NBATCH) load(b + 2, g[b & 1]);
         }
     }
+}
+
+// store_chunks for the 32x32 accumulator layout: lane (col, kg) holds row `col` of O^T in
+// o[db][4 jj + i] = dims 32 db + 8 jj + 4 kg + i.
+template <int DB, bool GATE>
+__device__ __forceinline__ void store_block(const f32x16 (&o)[DB], float inv, int kg, __amdgpu_buffer_rsrc_t o_rs,
+                                            int ooff, __amdgpu_buffer_rsrc_t g_rs, int goff) {
+    store_chunks<4 * DB, GATE>(
+        [&](int c) {
+            const int db = c >> 2, jj = c & 3;
+            return f32x4{o[db][4 * jj], o[db][4 * jj + 1], o[db][4 * jj + 2], o[db][4 * jj + 3]};
+        },
+        [&](int c) { return (c >> 2) * 32 + 8 * (c & 3) + 4 * kg; }, inv, o_rs, ooff, g_rs, goff);
 }
 
 }  // namespace pe

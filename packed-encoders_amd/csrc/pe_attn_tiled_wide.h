@@ -12,14 +12,15 @@
 
 namespace pe {
 
-// Workgroups per run that one XCD takes in a row: as many as its 32 CUs hold at once (one
-// workgroup per CU for head_dim 256, two for 128), in whole work entries (all head groups of
-// each). The launch rounds the grid up to whole rounds of 8 runs.
-template <int D>
-__host__ __device__ inline int wide_run(int hgroups) {
-    constexpr int kResident = D >= 256 ? 32 : 64;
-    return hgroups * (hgroups < kResident ? kResident / hgroups : 1);
+// Workgroups per run that one XCD takes in a row: as many as its 32 CUs hold at once
+// (RESIDENT), in whole work entries (all head groups of each). The launch rounds the grid up
+// to whole rounds of 8 runs.
+template <int RESIDENT>
+__host__ __device__ inline int xcd_run(int hgroups) {
+    return hgroups * (hgroups < RESIDENT ? RESIDENT / hgroups : 1);
 }
+// This kernel: two 64 KB workgroups per CU (head_dim 128).
+__host__ __device__ inline int wide_run(int hgroups) { return xcd_run<64>(hgroups); }
 
 template <int D, int G, int BN, int NS, bool GATE, bool WIN>
 __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
@@ -44,7 +45,7 @@ __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
     // XCD i % 8, and the runs of wide_run() consecutive items are dealt to the XCDs in turn,
     // so the tiles of a segment run side by side on one XCD and re-read its keys from that
     // XCD's L2 (dealt one item per XCD, every tile fetched them again from memory).
-    const int rh = wide_run<D>(p.hgroups);
+    const int rh = wide_run(p.hgroups);
     const int j = (int)(blockIdx.x >> 3);
     const int item = ((j / rh) * 8 + (int)(blockIdx.x & 7)) * rh + j % rh;
     const int entry = item / p.hgroups;

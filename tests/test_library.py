@@ -92,8 +92,12 @@ def test_workspace_size_is_host_arithmetic(lib):
     # every segment fits the short kernel: no workspace
     rc, size = _ws(lib, _args(max_seqlen=64))
     assert rc == 0 and size == 0
-    # GQA 4:1 packs 4 heads per tile: 32-row tiles
+    # GQA 4:1 packs 4 heads per tile; head_dim 256 tiles are four 16-row waves: 16-row tiles
     rc, size = _ws(lib, _args(n_heads_q=8, n_heads_kv=2, head_dim=256, max_seqlen=512, n_seq=256, total_tokens=71104))
+    assert rc == 0
+    assert size == 256 + 8 * min(256 * 32, (71104 + 256 * 15) // 16)
+    # head_dim 128 keeps 32-row waves: 4 heads of 32 rows
+    rc, size = _ws(lib, _args(n_heads_q=8, n_heads_kv=2, head_dim=128, max_seqlen=512, n_seq=256, total_tokens=71104))
     assert rc == 0
     assert size == 256 + 8 * min(256 * 16, (71104 + 256 * 31) // 32)
     # strips of 4 query tiles: min(N * ceil(ceil(S/128)/4), (tiles_by_tokens + N_long*3) // 4)
