@@ -6,8 +6,12 @@
 // runs per SIMD and every MFMA, exponential and memory latency is exposed (counters showed a
 // third of each wave's life waiting and a quarter stalled on dependencies). A 16-row block
 // halves both (64 + 32 registers), so two waves share each SIMD and cover each other's
-// latencies. The ring of direct global-to-LDS K/V stages, the swizzles, the Q steps and the
-// plan are those of the 32-row kernels; a query tile is 16 NW / G rows of each of G heads.
+// latencies. The ring of direct global-to-LDS K/V stages, the swizzles and the plan are those
+// of the 32-row kernels; a query tile is 16 NW / G rows of each of G heads. The Q fragment
+// (D / 8 registers) is loaded straight into registers rather than staged through the ring:
+// every ring step is a K/V step, and a workgroup's first wait covers its Q and its first
+// NS K/V tiles at once (the staged form paid one memory latency for Q, then another for the
+// first K/V tile, then ran a step with no products).
 //
 // Layouts (lane l: c16 = l % 16, g4 = l / 16). v_mfma_f32_16x16x32_bf16 takes A as 16 rows x
 // 32 k (lane: row c16, k 8 g4 .. 8 g4 + 7), B as 32 k x 16 columns (lane: column c16, the same
@@ -52,9 +56,7 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
     constexpr int TILE = BN * D;     // elements of one K (or V) tile
     constexpr int UPW = TILE / 8 / 64 / NW;  // 1 KB wave-loads per tensor per wave and step
     constexpr int LPS = 2 * UPW;     // loads per lane per step
-    constexpr int RQ = LPS * 64 / CPR;  // query rows per wave and Q step (a Q step loads as much as a K/V step)
-    constexpr int QS = 16 / RQ;      // Q steps per query tile
-    static_assert(QS * RQ == 16 && LPS % 4 == 0 && UPW % 2 == 0, "loads go out four at a time");
+    static_assert(LPS % 4 == 0 && UPW % 2 == 0, "loads go out four at a time");
 
     __shared__ __attribute__((aligned(16))) __bf16 ring[NS][2][TILE];
 
@@ -107,9 +109,7 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
     };
 
     // DMA geometry. K/V: wave-load j of this wave fills units [(wave * UPW + j) * 64, +64) of a
-    // tile; unit u holds key u / CPR, global 16-byte column (u % CPR) ^ swz(key). Q step i: the
-    // wave's RQ rows 16 rb + RQ i + r fill its RQ * D * 2-byte region of the stage, unit
-    // j * 64 + lane holding row r = unit / CPR, column (unit % CPR) ^ swz(r).
+    // tile; unit u holds key u / CPR, global 16-byte column (u % CPR) ^ swz(key).
     int koff[UPW], voff[UPW];
 #pragma unroll
     for (int jj = 0; jj < UPW; ++jj) {
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
         voff[jj] = key * v_row + ch * 16;
     }
     const uint32_t ring_base = uniform((int)lds_addr(&ring[0][0][0]));
-    constexpr uint32_t kStageBytes = 2 * TILE * 2, kTileBytes = TILE * 2, kQWaveBytes = RQ * D * 2;
+    constexpr uint32_t kStageBytes = 2 * TILE * 2, kTileBytes = TILE * 2;
     // LPS loads of one step (lds[i], off[i]); the first UPW read through ra, the rest rb.
     auto dma_step = [&](const uint32_t (&lds)[LPS], const int (&off)[LPS], __amdgpu_buffer_rsrc_t ra,
                         __amdgpu_buffer_rsrc_t rb) {
@@ -144,25 +144,6 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
         }
         dma_step(lds, off, k_rs, v_rs);
     };
-    // Q offsets are recomputed at each (rare) Q step rather than held in registers: the empty
-    // asm keeps the compiler from hoisting them out of the loop.
-    auto issue_q = [&](int stage, int qt, int i) {
-        const uint32_t qb = ring_base + stage * kStageBytes + wave * kQWaveBytes;
-        const int base = (qt * BM + rb * 16 + i * RQ) * q_row;
-        int ql = lane;
-        asm volatile("" : "+v"(ql));
-        uint32_t lds[LPS];
-        int off[LPS];
-#pragma unroll
-        for (int jj = 0; jj < LPS; ++jj) {
-            const int u = jj * 64 + ql;
-            const int r = u / CPR, ch = (u % CPR) ^ swz<CPR>(r);
-            lds[jj] = qb + jj * 1024;
-            off[jj] = base + r * q_row + ch * 16;
-        }
-        dma_step(lds, off, q_rs, q_rs);
-    };
-
     // Per-lane LDS read offsets (elements within a tile). swz<CPR>(key) = key & 15 for CPR 32.
     // K: key 16 kb + c16, unit (4 c + g4) ^ c16; with c = 4 ch + cl the XOR only touches cl,
     // so kaddr[cl] plus compile-time 16 kb D + 128 ch covers every (kb, c).
@@ -197,9 +178,18 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
     bool wave_active = r0 < L;
     int wr1 = min(L, r0 + 16);
     bf16x8 qf[DC];
-#pragma unroll
-    for (int c = 0; c < DC; ++c) qf[c] = bf16x8{};
     reset();
+
+    // Q fragment of query tile qt: lane (c16, g4) holds its row's dims 32 c + 8 g4 .. + 7. The
+    // loads are the compiler's (it places the wait before the first use); `force` makes that
+    // wait happen here, outside the step loop, so no step ever waits on a Q load.
+    auto load_q = [&](int qt_) {
+        const int base = (qt_ * BM + rb * 16 + c16) * q_row + 16 * g4;
+#pragma unroll
+        for (int c = 0; c < DC; ++c) qf[c] = buf_ld16(q_rs, base + 64 * c, 0);
+#pragma unroll
+        for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[c]));
+    };
 
     struct Cursor {
         int qt, t, klo, ntiles;
@@ -207,28 +197,26 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
     auto adv = [&](Cursor &c) {
         if (++c.t >= c.ntiles) {
             ++c.qt;
-            c.t = -QS;
+            c.t = 0;
             if (c.qt < qt_end) key_range(c.qt, c.klo, c.ntiles);
         }
     };
-    auto issue_step = [&](int stage, const Cursor &c) {
-        if (c.t < 0) issue_q(stage, c.qt, c.t + QS);
-        else issue_kv(stage, c.klo + c.t * BN);
-    };
 
-    // Prologue: issue the first NS - 1 steps.
-    Cursor ld{qt, -QS, klo, ntiles};
+    // Prologue: every stage is free, so the first NS K/V tiles go out, then the Q fragment
+    // (whose wait therefore covers them too: one memory latency for the workgroup's start).
+    Cursor ld{qt, 0, klo, ntiles};
     int issued = 0;
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) {
+    for (int s = 0; s < NS; ++s) {
         if (ld.qt < qt_end) {
-            issue_step(issued % NS, ld);
+            issue_kv(issued % NS, ld.klo + ld.t * BN);
             ++issued;
             adv(ld);
         }
     }
+    load_q(qt);
 
-    int t = -QS, step = 0;
+    int t = 0, step = 0;
     while (true) {
         // This step's loads are complete once at most the later steps' loads are in flight
         // (loads complete in issue order; other outstanding accesses only make this stricter).
@@ -238,28 +226,15 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
         else wait_vmcnt<0>();
         __syncthreads();
         // Refill the stage freed by the previous step (all waves passed the barrier after it).
-        if (ld.qt < qt_end) {
-            issue_step(issued % NS, ld);
+        if (step > 0 && ld.qt < qt_end) {
+            issue_kv(issued % NS, ld.klo + ld.t * BN);
             ++issued;
             adv(ld);
         }
 
         const __bf16 *kt = &ring[step % NS][0][0];
-        if (t < 0) {
-            // Q step t + QS: lanes whose row is in this step's part read their fragment.
-            const int i = t + QS;
-            if (QS == 1 || c16 / RQ == i) {
-                const int r = c16 % RQ;
-                const __bf16 *qs = kt + wave * RQ * D + r * D;
-#pragma unroll
-                for (int c = 0; c < DC; ++c) qf[c] = ld_s16(qs + ((4 * c + g4) ^ r) * 8);
-#pragma unroll
-                for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[c]));
-            }
-        }
-
         const __bf16 *vt = &ring[step % NS][1][0];
-        if (t >= 0 && wave_active) {
+        if (wave_active) {
             const int kt0 = klo + t * BN;
             if (block_live(kt0, Lk, r0 + off, wr1 + off, wl, wr)) {
                 f32x4 s[2];
@@ -314,7 +289,7 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
             }
         }
 
-        if (t >= 0 && t + 1 >= ntiles) {
+        if (t + 1 >= ntiles) {
             // Last key tile of this query tile: normalise, apply the gate, store, reset.
             float lt = (ls[0] + ls[1]) + (ls[2] + ls[3]);
             lt += __shfl_xor(lt, 16);
@@ -334,7 +309,8 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
             myrow = r0 + c16;
             wave_active = r0 < L;
             wr1 = min(L, r0 + 16);
-            t = -QS;
+            load_q(qt);  // waits here (and for the ring's loads in flight): strips of several tiles only
+            t = 0;
         } else {
             ++t;
         }
