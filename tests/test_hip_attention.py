@@ -354,6 +354,56 @@ def test_window_gate_and_short_routing(pe, window, causal):
     _assert_parity(got, want, cu)
 
 
+WIDE_LENGTHS = [1, 15, 16, 17, 31, 32, 33, 100, 255, 257, 513, 0, 2]
+WIDE_CASES = [((-1, -1), False), ((-1, -1), True), ((64, 64), False), ((0, 0), False), ((15, 17), False),
+              ((100, -1), True), ((33, 0), False)]
+
+
+@pytest.mark.parametrize("window,causal", WIDE_CASES, ids=[f"{w[0]}_{w[1]}{'c' if c else ''}" for w, c in WIDE_CASES])
+def test_head_dim_256_windows_strips_and_gate(pe, window, causal):
+    """head_dim 256 (16-row query blocks, four heads per kv head, 32-key steps): windows and
+    causal bounds of every alignment against the 16-row blocks and 32-key steps (lengths
+    straddle both edges, an empty segment included), with the fused gate; strips of three and
+    of eight query tiles per workgroup are bit-identical to one-tile workgroups."""
+    from packed_encoders_amd import _lib
+
+    announce(f"head_dim 256 window={window} causal={causal}")
+    q, k, v, cu, gt = _inputs(WIDE_LENGTHS, hq=8, hkv=2, d=256, seed=71, gate=True)
+    qd, kd, vd, cud, gd = _dev(q, k, v, cu, gt)
+    lib = _lib.library()
+    mx = max(WIDE_LENGTHS)
+    got = _launch(lib, qd, kd, vd, cud, mx, window, causal, gate=gd)
+    want = _oracle(q, k, v, cu, scale=0.125, window=window, causal=causal, gate=gt)
+    _assert_parity(got, want, cu)
+    for strip in (3, 8):
+        assert torch.equal(_launch(lib, qd, kd, vd, cud, mx, window, causal, gate=gd, strip=strip), got)
+
+
+@pytest.mark.parametrize("jump", [0.25, 1.0, 10.0], ids=["below-lazy", "rescale", "far"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_head_dim_256_rescales_on_rising_scores(pe, jump, causal):
+    """head_dim 256 keeps the exact running maximum of every key tile and rescales lazily (only
+    when a tile's maximum exceeds it by more than 8 in log2 units): keys 40..109 of a segment
+    score about 18 * jump log2 units above the rest (|q| . jump over 256 dims at scale 1/16),
+    so jump 0.25 stays under the threshold (unnormalised probabilities up to ~2^5 kept), 1.0
+    rescales mid-segment at a block edge, and 10.0 underflows every earlier probability; all
+    must match the oracle."""
+    lengths = [300, 129, 64]
+    announce(f"head_dim 256 score jump={jump} causal={causal}")
+    q, k, v, cu, _ = _inputs(lengths, hq=8, hkv=2, d=256, seed=73)
+    q = q.float().abs().bfloat16()
+    k = k.float()
+    for a in (0, 300):
+        k[a + 40:a + 110] = jump
+    k = k.bfloat16()
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    with torch.inference_mode():
+        got = pe.varlen_attention(qd, kd, vd, cud, max(lengths), softmax_scale=1.0 / 16, causal=causal,
+                                  short_max=0)
+    want = _oracle(q, k, v, cu, scale=1.0 / 16, causal=causal)
+    _assert_parity(got, want, cu)
+
+
 PREFIX_Q = [5, 1, 37, 16, 130, 300, 64, 20, 0, 7, 260]
 PREFIX_K = [40, 64, 37, 80, 700, 300, 200, 5, 50, 7, 1000]  # the reference's probe pairs, then longer
 
