@@ -172,33 +172,49 @@ __device__ __forceinline__ bool block_full(int kb0, int L, int r0, int r1, int w
     return true;
 }
 
-// Round 4 fp32 outputs to bf16 and apply the optional fused sigmoid gate (g holds the gate's
-// 4 bf16 values): y = bf16(bf16(o) * bf16(sigmoid(g))), the rounding order of the reference's
-// gate kernel (packed_encoders/_kernels/hybrid.py:197-206). Roundings go two at a time
-// (v_cvt_pk_bf16_f32). The sigmoid's reciprocal is v_rcp_f32 (1 ulp) rather than an IEEE
-// division (about ten instructions): its result is rounded to bf16 next, which a 1-ulp fp32
-// difference can move by one bf16 step only when the quotient lies within that ulp of a
-// rounding boundary.
-template <bool GATE>
-__device__ __forceinline__ bf16x4 out4(float a0, float a1, float a2, float a3, bf16x4 g) {
+// Output rounding and the optional fused sigmoid gate: y = bf16(bf16(o) * bf16(sigmoid(g))),
+// the rounding order of the reference's gate kernel (packed_encoders/_kernels/hybrid.py:197-206).
+// Roundings go two at a time (v_cvt_pk_bf16_f32). The sigmoid's reciprocal is v_rcp_f32
+// (1 ulp) rather than an IEEE division (about ten instructions): its result is rounded to bf16
+// next, which a 1-ulp fp32 difference can move by one bf16 step only when the quotient lies
+// within that ulp of a rounding boundary.
+
+// bf16(sigmoid(g)) of 4 gate values.
+__device__ __forceinline__ bf16x4 sigmoid4(bf16x4 g) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    float sg[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sg[i] = __builtin_amdgcn_rcpf(1.0f + __expf(-(float)g[i]));
+    const bf16x2 s01 = __builtin_convertvector(f32x2{sg[0], sg[1]}, bf16x2);
+    const bf16x2 s23 = __builtin_convertvector(f32x2{sg[2], sg[3]}, bf16x2);
+    return bf16x4{s01[0], s01[1], s23[0], s23[1]};
+}
+
+// bf16(bf16(a) * s) for 4 outputs a and 4 bf16 gate factors s (SCALED), or bf16(a).
+template <bool SCALED>
+__device__ __forceinline__ bf16x4 round4(float a0, float a1, float a2, float a3, bf16x4 s) {
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     typedef float f32x2 __attribute__((ext_vector_type(2)));
     const bf16x2 r01 = __builtin_convertvector(f32x2{a0, a1}, bf16x2);
     const bf16x2 r23 = __builtin_convertvector(f32x2{a2, a3}, bf16x2);
-    if constexpr (!GATE) {
+    if constexpr (!SCALED) {
         return bf16x4{r01[0], r01[1], r23[0], r23[1]};
     } else {
-        float sg[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sg[i] = __builtin_amdgcn_rcpf(1.0f + __expf(-(float)g[i]));
-        const bf16x2 s01 = __builtin_convertvector(f32x2{sg[0], sg[1]}, bf16x2);
-        const bf16x2 s23 = __builtin_convertvector(f32x2{sg[2], sg[3]}, bf16x2);
+        const bf16x2 s01 = {s[0], s[1]}, s23 = {s[2], s[3]};
         const bf16x2 y01 = __builtin_convertvector(
             __builtin_convertvector(r01, f32x2) * __builtin_convertvector(s01, f32x2), bf16x2);
         const bf16x2 y23 = __builtin_convertvector(
             __builtin_convertvector(r23, f32x2) * __builtin_convertvector(s23, f32x2), bf16x2);
         return bf16x4{y01[0], y01[1], y23[0], y23[1]};
     }
+}
+
+// round4 of 4 outputs with the gate's sigmoid taken here from its 4 raw values g (GATE).
+template <bool GATE>
+__device__ __forceinline__ bf16x4 out4(float a0, float a1, float a2, float a3, bf16x4 g) {
+    if constexpr (!GATE) return round4<false>(a0, a1, a2, a3, g);
+    else return round4<true>(a0, a1, a2, a3, sigmoid4(g));
 }
 
 // Epilogue of a wave's query block: NCH chunks of 4 consecutive dims of the lane's query row,

@@ -180,15 +180,31 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
     bf16x8 qf[DC];
     reset();
 
-    // Q fragment of query tile qt: lane (c16, g4) holds its row's dims 32 c + 8 g4 .. + 7. The
-    // loads are the compiler's (it places the wait before the first use); `force` makes that
-    // wait happen here, outside the step loop, so no step ever waits on a Q load.
-    auto load_q = [&](int qt_) {
-        const int base = (qt_ * BM + rb * 16 + c16) * q_row + 16 * g4;
+    // Inputs of query tile qt held in registers: the Q fragment (lane (c16, g4): its row's dims
+    // 32 c + 8 g4 .. + 7) and, with a gate, bf16(sigmoid(gate)) of the dims it stores (16 db +
+    // 4 g4 + i). The loads are the compiler's (it places the wait before the first use); the
+    // empty asm makes that wait, and the sigmoids, happen here, outside the step loop: no step
+    // waits on these loads, and the epilogue only scales, rounds and stores (the sigmoids run
+    // while the CU's other workgroup is in its steps).
+    bf16x4 sgv[GATE ? DB : 1];
+    auto load_tile_inputs = [&](int qt_) {
+        const int row = qt_ * BM + rb * 16 + c16;
+        const int base = row * q_row + 16 * g4;
 #pragma unroll
         for (int c = 0; c < DC; ++c) qf[c] = buf_ld16(q_rs, base + 64 * c, 0);
+        if constexpr (GATE) {
+            const int gbase = row * (int)p.g_st * 2 + 8 * g4;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) sgv[db] = buf_ld8(g_rs, gbase + 32 * db, 0);
+        }
 #pragma unroll
         for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[c]));
+        if constexpr (GATE) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db) sgv[db] = sigmoid4(sgv[db]);
+#pragma unroll
+            for (int db = 0; db < DB; ++db) asm volatile("" : "+v"(sgv[db]));
+        }
     };
 
     struct Cursor {
@@ -202,8 +218,8 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
         }
     };
 
-    // Prologue: every stage is free, so the first NS K/V tiles go out, then the Q fragment
-    // (whose wait therefore covers them too: one memory latency for the workgroup's start).
+    // Prologue: every stage is free, so the first NS K/V tiles go out, then the tile's register
+    // inputs (whose wait therefore covers them too: one memory latency for the workgroup's start).
     Cursor ld{qt, 0, klo, ntiles};
     int issued = 0;
 #pragma unroll
@@ -214,7 +230,7 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
             adv(ld);
         }
     }
-    load_q(qt);
+    load_tile_inputs(qt);
 
     int t = 0, step = 0;
     while (true) {
@@ -296,10 +312,12 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
             lt += __shfl_xor(lt, 32);
             if (wave_active) {
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-                const int ooff = myrow * (int)p.o_st * 2;
-                const int goff = GATE ? myrow * (int)p.g_st * 2 : 0;
-                store_chunks<DB, GATE>([&](int db) { return o[db]; }, [&](int db) { return 16 * db + 4 * g4; }, inv,
-                                       o_rs, ooff, g_rs, goff);
+                const int ooff = myrow * (int)p.o_st * 2 + 8 * g4;
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    buf_st8(o_rs, ooff + 32 * db,
+                            round4<GATE>(o[db][0] * inv, o[db][1] * inv, o[db][2] * inv, o[db][3] * inv,
+                                         sgv[GATE ? db : 0]));
             }
             reset();
             if (qt + 1 >= qt_end) break;
@@ -309,7 +327,7 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
             myrow = r0 + c16;
             wave_active = r0 < L;
             wr1 = min(L, r0 + 16);
-            load_q(qt);  // waits here (and for the ring's loads in flight): strips of several tiles only
+            load_tile_inputs(qt);  // waits here (and for the ring's loads in flight): strips of several tiles only
             t = 0;
         } else {
             ++t;
