@@ -49,28 +49,129 @@ __device__ __forceinline__ int plan_bucket(int cost) {
     return min(63, 2 * lg + half);
 }
 
+// Segments of more than kSerialStrips strips are planned by a whole wave, lanes over strips
+// (a thread per segment walked a 64-strip segment serially: ~20 us for C4's 16 segments); up
+// to kWaveQueue of them are queued in LDS with their lengths (a wave then reads no global
+// memory per segment), and past that every segment is planned serially. Shorter segments stay
+// one per thread: a wave's pass over one segment is a chain of LDS round trips (~1.5 us), so
+// C5's 256 segments of up to 32 strips took 40 us by waves against 13 us by threads.
+constexpr int kSerialStrips = 32;
+constexpr int kWaveQueue = 2048;
+
 // One entry per strip of `strip` consecutive query tiles of `bm` rows: (segment, first tile).
 // Segment s has cu[s + 1] - cu[s] query rows and cuk[s + 1] - cuk[s] keys (cuk = cu when the
-// two share boundaries); it is the short kernel's when both fit short_max.
+// two share boundaries); it is the short kernel's when both fit short_max. Pass 1 counts
+// entries per cost bucket, pass 2 reserves contiguous runs and writes them; both passes plan
+// each segment the same way (serially or by a wave), and a run's reservation is the same in
+// either.
 __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int32_t *cuk, int n_seq, int short_max,
                                                     int bm, int strip, int wl, int wr, int group, int2 *work,
                                                     int32_t *count, int cap) {
     __shared__ int cnt[64];
     __shared__ int off[64];
+    __shared__ int3 queue[kWaveQueue];  // (segment, query rows, keys)
+    __shared__ int queued;
     const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
     if (tid < 64) cnt[tid] = 0;
+    if (tid == 0) queued = 0;
     __syncthreads();
+
+    auto strips_of = [&](int seg, int &L, int &Lk, int &nq, int &ns) {
+        L = cu[seg + 1] - cu[seg];
+        Lk = cuk[seg + 1] - cuk[seg];
+        nq = (L + bm - 1) / bm;
+        ns = (nq + strip - 1) / strip;
+        return max(L, Lk) > short_max;  // the tiled kernel's
+    };
     for (int seg = tid; seg < n_seq; seg += blockDim.x) {
-        const int L = cu[seg + 1] - cu[seg], Lk = cuk[seg + 1] - cuk[seg];
-        if (max(L, Lk) <= short_max) continue;
+        int L, Lk, nq, ns;
+        if (strips_of(seg, L, Lk, nq, ns) && ns > kSerialStrips) {
+            const int qi = atomicAdd(&queued, 1);
+            if (qi < kWaveQueue) queue[qi] = make_int3(seg, L, Lk);
+        }
+    }
+    __syncthreads();
+    const bool by_wave = queued <= kWaveQueue;  // else every segment serially
+    const int nqueued = by_wave ? queued : 0;
+
+    // One thread plans segment seg: pass 1 (place = false) counts, pass 2 writes.
+    auto serial_segment = [&](int seg, bool place) {
+        int L, Lk, nq, ns;
+        if (!strips_of(seg, L, Lk, nq, ns) || (by_wave && ns > kSerialStrips)) return;
+        if (group) {
+            const int b = plan_bucket(plan_segment_cost(ns, strip, nq, bm, L, Lk, wl, wr));
+            if (!place) {
+                atomicAdd(&cnt[b], ns);
+                return;
+            }
+            // Strips in decreasing cost: the causal / end-aligned prefix grows with the strip.
+            const int pos = atomicAdd(&off[b], ns);
+            const bool rev =
+                plan_strip_cost(ns - 1, strip, nq, bm, L, Lk, wl, wr) > plan_strip_cost(0, strip, nq, bm, L, Lk, wl, wr);
+            for (int i = 0; i < ns; ++i)
+                if (pos + i < cap) work[pos + i] = make_int2(seg, (rev ? ns - 1 - i : i) * strip);
+            return;
+        }
+        int s = 0;
+        while (s < ns) {
+            // A run of consecutive strips in one cost bucket gets one contiguous reservation.
+            const int b = plan_bucket(plan_strip_cost(s, strip, nq, bm, L, Lk, wl, wr));
+            int e = s + 1;
+            while (e < ns && plan_bucket(plan_strip_cost(e, strip, nq, bm, L, Lk, wl, wr)) == b) ++e;
+            if (!place) {
+                atomicAdd(&cnt[b], e - s);
+            } else {
+                const int pos = atomicAdd(&off[b], e - s);
+                for (int i = 0; i < e - s; ++i)
+                    if (pos + i < cap) work[pos + i] = make_int2(seg, (s + i) * strip);
+            }
+            s = e;
+        }
+    };
+    // A wave plans segment seg (wave-uniform), lane i taking strips i, i + 64, ...: runs of
+    // equal buckets within each 64-strip chunk are found with a ballot, one atomic per run.
+    auto wave_segment = [&](int3 q, bool place) {
+        const int seg = q.x, L = q.y, Lk = q.z;
         const int nq = (L + bm - 1) / bm;
         const int ns = (nq + strip - 1) / strip;
         if (group) {
-            atomicAdd(&cnt[plan_bucket(plan_segment_cost(ns, strip, nq, bm, L, Lk, wl, wr))], ns);
-            continue;
+            int64_t c = 0;
+            for (int s = lane; s < ns; s += 64) c += plan_strip_cost(s, strip, nq, bm, L, Lk, wl, wr);
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) c += __shfl_xor(c, d);
+            const int b = plan_bucket((int)min(c, (int64_t)0x7fffffff));
+            int pos = 0;
+            if (lane == 0) pos = place ? atomicAdd(&off[b], ns) : atomicAdd(&cnt[b], ns);
+            if (!place) return;
+            pos = __shfl(pos, 0);
+            const bool rev =
+                plan_strip_cost(ns - 1, strip, nq, bm, L, Lk, wl, wr) > plan_strip_cost(0, strip, nq, bm, L, Lk, wl, wr);
+            for (int i = lane; i < ns; i += 64)
+                if (pos + i < cap) work[pos + i] = make_int2(seg, (rev ? ns - 1 - i : i) * strip);
+            return;
         }
-        for (int s = 0; s < ns; ++s) atomicAdd(&cnt[plan_bucket(plan_strip_cost(s, strip, nq, bm, L, Lk, wl, wr))], 1);
-    }
+        for (int s0 = 0; s0 < ns; s0 += 64) {
+            const int s = s0 + lane;
+            const bool valid = s < ns;
+            const int b = valid ? plan_bucket(plan_strip_cost(s, strip, nq, bm, L, Lk, wl, wr)) : -1;
+            const int prev = __shfl_up(b, 1);
+            const bool start = valid && (lane == 0 || b != prev);
+            const uint64_t starts = __ballot(start);
+            const uint64_t after = lane == 63 ? 0ull : starts >> (lane + 1);
+            const int next = after ? lane + __ffsll((long long)after) : min(64, ns - s0);
+            int pos = 0;
+            if (start) pos = place ? atomicAdd(&off[b], next - lane) : atomicAdd(&cnt[b], next - lane);
+            if (!place) continue;
+            const uint64_t upto = starts & (lane == 63 ? ~0ull : (2ull << lane) - 1);
+            const int rs = 63 - __clzll((long long)upto);  // this lane's run start
+            const int p0 = __shfl(pos, rs);
+            if (valid && p0 + (lane - rs) < cap) work[p0 + lane - rs] = make_int2(seg, s * strip);
+        }
+    };
+
+    for (int seg = tid; seg < n_seq; seg += blockDim.x) serial_segment(seg, false);
+    for (int i = wave; i < nqueued; i += nwaves) wave_segment(queue[i], false);
     __syncthreads();
     if (tid == 0) {
         int run = 0;
@@ -81,32 +182,8 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
         *count = min(run, cap);
     }
     __syncthreads();
-    for (int seg = tid; seg < n_seq; seg += blockDim.x) {
-        const int L = cu[seg + 1] - cu[seg], Lk = cuk[seg + 1] - cuk[seg];
-        if (max(L, Lk) <= short_max) continue;
-        const int nq = (L + bm - 1) / bm;
-        const int ns = (nq + strip - 1) / strip;
-        if (group) {
-            // Strips in decreasing cost: the causal / end-aligned prefix grows with the strip.
-            const int pos = atomicAdd(&off[plan_bucket(plan_segment_cost(ns, strip, nq, bm, L, Lk, wl, wr))], ns);
-            const bool rev =
-                plan_strip_cost(ns - 1, strip, nq, bm, L, Lk, wl, wr) > plan_strip_cost(0, strip, nq, bm, L, Lk, wl, wr);
-            for (int i = 0; i < ns; ++i)
-                if (pos + i < cap) work[pos + i] = make_int2(seg, (rev ? ns - 1 - i : i) * strip);
-            continue;
-        }
-        int s = 0;
-        while (s < ns) {
-            // A run of consecutive strips in one cost bucket gets one contiguous reservation.
-            const int b = plan_bucket(plan_strip_cost(s, strip, nq, bm, L, Lk, wl, wr));
-            int e = s + 1;
-            while (e < ns && plan_bucket(plan_strip_cost(e, strip, nq, bm, L, Lk, wl, wr)) == b) ++e;
-            const int pos = atomicAdd(&off[b], e - s);
-            for (int i = 0; i < e - s; ++i)
-                if (pos + i < cap) work[pos + i] = make_int2(seg, (s + i) * strip);
-            s = e;
-        }
-    }
+    for (int seg = tid; seg < n_seq; seg += blockDim.x) serial_segment(seg, true);
+    for (int i = wave; i < nqueued; i += nwaves) wave_segment(queue[i], true);
 }
 
 }  // namespace pe

@@ -354,6 +354,34 @@ def test_window_gate_and_short_routing(pe, window, causal):
     _assert_parity(got, want, cu)
 
 
+@pytest.mark.parametrize("window,causal", [((-1, -1), False), ((64, 64), False), ((-1, -1), True), ((200, 7), False)],
+                         ids=["global", "band64", "causal", "asym"])
+def test_long_segments_planned_by_waves(pe, window, causal):
+    """Segments of more than 32 strips are planned by a whole wave (lanes over strips, runs of
+    equal cost buckets found per 64-strip chunk): 9,000 and 4,500 tokens give 71 and 36
+    query tiles of 128 rows, whose band-edge and causal costs split runs inside and across the
+    chunks. Every row must be written exactly once (the output starts as 3.0 everywhere) and
+    sampled rows, including every tile edge of the long segment, match the oracle."""
+    from packed_encoders_amd import _lib
+
+    lengths = [3, 9000, 4500, 200]
+    announce(f"wave-planned long segments window={window} causal={causal}")
+    q, k, v, cu, _ = _inputs(lengths, hq=2, seed=79)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    got = _launch(_lib.library(), qd, kd, vd, cud, max(lengths), window, causal)
+    live = int(cu[-1])
+    written = ~(got[:live].float() == 3.0).all(dim=-1).all(dim=-1)
+    assert bool(written.all()), f"{int((~written).sum())} rows never written"
+    edges = [3 + 128 * t + d for t in range(71) for d in (0, 127) if 128 * t + d < 9000]
+    rows = np.unique(np.array(edges + [0, 1, 2] + list(range(9003, live, 97)) + [live - 1]))
+    f = lambda t: t.float().numpy()
+    want = oa.sampled_rows_attention(f(q), f(k), f(v), cu.numpy(), rows, scale=0.125, window=window, causal=causal)
+    err = np.abs(got.float().cpu().numpy()[rows] - want)
+    assert err.max() <= MAX_ABS, f"max abs {err.max():.4g}"
+    cos = oa.cosine_per_token(got.float().cpu().numpy()[rows].astype(np.float64), want)
+    assert cos.min() >= MIN_COS, f"min cosine {cos.min():.6f}"
+
+
 WIDE_LENGTHS = [1, 15, 16, 17, 31, 32, 33, 100, 255, 257, 513, 0, 2]
 WIDE_CASES = [((-1, -1), False), ((-1, -1), True), ((64, 64), False), ((0, 0), False), ((15, 17), False),
               ((100, -1), True), ((33, 0), False)]
