@@ -10,7 +10,7 @@
 // neighbouring workgroups. With `group` set, the unit of ordering is the whole segment:
 // its strips are one contiguous reservation (costliest strip first), bucketed by the
 // segment's total cost, so a run of neighbouring workgroups holds every query tile of a
-// segment and re-reads its keys from one L2 (the head_dim 128 / 256 kernel deals such runs
+// segment and re-reads its keys from one L2 (the head_dim 128 and 256 kernels deal such runs
 // to the XCDs). Order within a bucket depends on atomics; it changes only the schedule,
 // never a result: every output row is produced by exactly one workgroup.
 #pragma once

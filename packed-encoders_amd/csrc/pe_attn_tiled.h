@@ -1,5 +1,6 @@
 // Tiled flash-style packed attention for long segments, head_dim 64 (gfx950 MFMA); wider
-// heads use wide_attn_kernel (pe_attn_tiled_wide.h), which shares the staging below.
+// heads use wide_attn_kernel (head_dim 128, pe_attn_tiled_wide.h) and wide16_attn_kernel
+// (head_dim 256, pe_attn_tiled_wide16.h), which share the staging below.
 //
 // One workgroup = 4 waves = one strip of consecutive query tiles of one segment, for one group
 // of G query heads. A query tile has 32*4/G rows: the G heads share one kv head (G divides the
@@ -65,7 +66,7 @@ constexpr int kXcdRun = 4;
 // kernel names in traces.
 template <int D, int G, int BN, int NS, bool GATE, bool WIN>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void tiled_attn_kernel(AttnParams p) {
-    static_assert(D == 64 && BN == 64 && NS == 3, "head_dim 64 kernel (wider heads: wide_attn_kernel)");
+    static_assert(D == 64 && BN == 64 && NS == 3, "head_dim 64 kernel (wider heads: wide_attn_kernel, wide16_attn_kernel)");
     static_assert(D % 32 == 0 && BN % 32 == 0 && (4 % G) == 0 && NS >= 2, "tile shape");
     constexpr int WPH = 4 / G;       // waves per query head
     constexpr int BM = 32 * WPH;     // query rows per query tile

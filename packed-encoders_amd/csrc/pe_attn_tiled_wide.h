@@ -1,4 +1,5 @@
-// Tiled packed attention for head_dim 128 and 256 (gfx950 MFMA): the same workgroup shape,
+// Tiled packed attention for head_dim 128 (gfx950 MFMA; head_dim 256 runs the 16-row
+// wide16_attn_kernel, pe_attn_tiled_wide16.h, built on this one): the same workgroup shape,
 // LDS ring, direct global-to-LDS staging, Q steps, swizzles and buffer-bounded accesses as
 // tiled_attn_kernel (pe_attn_tiled.h), with a step loop shaped for the register budget of
 // wide heads, whose O accumulators alone take D / 2 VGPRs per lane: one copy of the step (the
