@@ -111,7 +111,8 @@ def test_varlen_attention_matches_oracle(pe, lengths, window, causal, short_max)
     _assert_parity(got, want, cu)
 
 
-@pytest.mark.parametrize("d,hq,hkv", [(64, 8, 2), (128, 6, 3), (128, 4, 4), (256, 8, 2), (256, 8, 1), (64, 16, 2)])
+@pytest.mark.parametrize("d,hq,hkv", [(64, 8, 2), (128, 6, 3), (128, 4, 4), (256, 8, 2), (256, 8, 1), (64, 16, 2),
+                                      (256, 4, 4), (256, 6, 3)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_gqa_head_dims(pe, d, hq, hkv, causal):
     lengths = [16, 200, 5, 77, 512]
