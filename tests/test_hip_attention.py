@@ -269,18 +269,20 @@ def test_out_of_envelope_raises_value_error(pe):
             pe.varlen_attention(q.float(), k, v, cu, 32)
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("window,causal", [((-1, -1), False), ((64, 64), False), ((-1, -1), True), ((5, 130), False)],
                          ids=["global", "band64", "causal", "asym"])
-def test_strips_are_bit_identical_and_match_oracle(pe, window, causal):
+def test_strips_are_bit_identical_and_match_oracle(pe, window, causal, d):
     """A workgroup walking a strip of query tiles computes every row exactly as a one-tile
     workgroup does: outputs are bit-identical for every strip length (including strips that
-    cross into a segment's last, partial tile) and match the oracle."""
+    cross into a segment's last, partial tile) and match the oracle (head_dim 64 and the
+    head_dim 128 kernel)."""
     from packed_encoders_amd import _lib
     from packed_encoders_amd.hip_attention import _args
 
     lengths = [700, 65, 1500, 129, 5, 1024]
-    announce(f"strips window={window} causal={causal}")
-    q, k, v, cu, _ = _inputs(lengths, hq=4, hkv=2, seed=31)
+    announce(f"strips window={window} causal={causal} d={d}")
+    q, k, v, cu, _ = _inputs(lengths, hq=4, hkv=2, d=d, seed=31)
     qd, kd, vd, cud = _dev(q, k, v, cu)
     lib = _lib.library()
     outs = {}
