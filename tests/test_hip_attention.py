@@ -466,6 +466,29 @@ def test_separate_key_segments_match_oracle(pe, window, causal, d, hq, hkv, shor
     _assert_parity(got, want, cu_q)
 
 
+@pytest.mark.parametrize("d,hq,hkv,short_max", [(64, 4, 4, 64), (128, 4, 2, 0), (256, 8, 2, 0)])
+def test_separate_key_segments_with_gate(pe, d, hq, hkv, short_max):
+    """The prefixed form with the fused sigmoid gate (the gated hybrid layers continuing a
+    shared prefix): causal rows at their key positions, gate applied per query row, rows with
+    no key written as zero (the gate of a zero output is still zero)."""
+    announce(f"separate key segments with gate d={d} heads={hq}/{hkv} short_max={short_max}")
+    g = torch.Generator().manual_seed(83)
+    q = torch.randn(sum(PREFIX_Q), hq, d, generator=g).bfloat16()
+    k = torch.randn(sum(PREFIX_K), hkv, d, generator=g).bfloat16()
+    v = torch.randn(sum(PREFIX_K), hkv, d, generator=g).bfloat16()
+    gt = torch.randn(sum(PREFIX_Q), hq, d, generator=g).bfloat16()
+    cu_q = torch.tensor([0, *np.cumsum(PREFIX_Q).tolist()], dtype=torch.int32)
+    cu_k = torch.tensor([0, *np.cumsum(PREFIX_K).tolist()], dtype=torch.int32)
+    qd, kd, vd, cqd, ckd, gd = _dev(q, k, v, cu_q, cu_k, gt)
+    with torch.inference_mode():
+        got = pe.varlen_attention(qd, kd, vd, cqd, max(PREFIX_Q), softmax_scale=0.125, causal=True, gate=gd,
+                                  short_max=short_max, cu_seqlens_k=ckd, max_seqlen_k=max(PREFIX_K))
+    f = lambda t: t.float().numpy()
+    want = oa.packed_attention(f(q), f(k), f(v), cu_q.numpy(), scale=0.125, causal=True, gate=f(gt),
+                               cu_seqlens_k=cu_k.numpy())
+    _assert_parity(got, want, cu_q)
+
+
 @pytest.mark.parametrize("jump", [4.0, 10.0], ids=["below-guard", "past-guard"])
 @pytest.mark.parametrize("window,causal", [((-1, -1), False), ((64, 64), False), ((-1, -1), True)],
                          ids=["global", "band64", "causal"])
