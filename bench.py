@@ -326,8 +326,24 @@ def cpu_threads() -> int:
     return max(1, cores)
 
 
-def cpu_bench(workload, repeats: int = 3):
-    """The same attention schedule on the host CPU (fp32), timed after one warm-up."""
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def cpu_bench(workload, repeats: int = 7):
+    """The same attention schedule on the host CPU (fp32): one warm-up, then the median of
+    ``repeats`` timed steps on all physical cores (benchmarks/cpu/README.md:27-31), and a
+    1-thread run on a bounded sample (the first global and the first banded layer, median of
+    3) scaled to the same unit."""
     import numpy as np
     import torch
     import torch.nn.functional as F
@@ -338,7 +354,6 @@ def cpu_bench(workload, repeats: int = 3):
     cpu.build()
     kind = "reference" if cpu.available("reference") and workload.head_dim == 64 else "port"
     threads = cpu_threads()
-    torch.set_num_threads(threads)
     T, hq, d = workload.total_tokens, workload.n_heads_q, workload.head_dim
     if workload.n_heads_kv != hq:
         return None
@@ -350,14 +365,14 @@ def cpu_bench(workload, repeats: int = 3):
     longest = max(lengths)
     offsets = np.concatenate([[0], np.cumsum(lengths)])
 
-    def layer_call(layer):
+    def layer_call(layer, n_threads):
         if layer.causal or layer.gate or layer.window[0] != layer.window[1]:
             raise ValueError("CPU baseline covers symmetric bands and global attention")
         if layer.window != (-1, -1):
-            cpu.local_attention(qn, kn, vn, lengths, layer.window[0], kind=kind, threads=threads, out=out,
+            cpu.local_attention(qn, kn, vn, lengths, layer.window[0], kind=kind, threads=n_threads, out=out,
                                 scale=workload.scale)
         elif longest <= 128:
-            cpu.local_attention(qn, kn, vn, lengths, longest, kind=kind, threads=threads, out=out,
+            cpu.local_attention(qn, kn, vn, lengths, longest, kind=kind, threads=n_threads, out=out,
                                 scale=workload.scale)
         else:  # per-segment fp32 SDPA, as the reference's CPU engine does for long global layers
             with torch.inference_mode():
@@ -365,25 +380,41 @@ def cpu_bench(workload, repeats: int = 3):
                     F.scaled_dot_product_attention(q[None, :, a:b], k[None, :, a:b], v[None, :, a:b],
                                                    scale=workload.scale)
 
-    def run():
-        for layer in workload.layers:
-            layer_call(layer)
+    def timed(layers, n_threads, n):
+        torch.set_num_threads(n_threads)
+        for layer in layers:  # warm-up
+            layer_call(layer, n_threads)
+        times = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            for layer in layers:
+                layer_call(layer, n_threads)
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times)
 
-    run()
-    times = []
-    for _ in range(repeats):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    seconds = statistics.median(times)
+    seconds = timed(workload.layers, threads, repeats)
     flops = sum(hip.useful_flops(lengths, hq, d, window=l.window) for l in workload.layers)
-    sample = (f"full {workload.name} schedule ({len(workload.layers)} attention layers, T={T}) in fp32, "
-              f"median of {repeats} after 1 warm-up; band/short layers: "
-              f"{'reference pe_local_attention (oracle/_ref)' if kind == 'reference' else 'oracle C port'}; "
-              f"global layers longer than 128: per-segment torch SDPA")
-    log(f"cpu baseline ({kind}, {threads} threads): {seconds * 1e3:.1f} ms/step -> {flops / seconds / 1e12:.3f} TFLOP/s")
+    # 1 thread: one layer of each kind present, scaled by its share of the schedule's FLOPs
+    kinds = []
+    for layer in workload.layers:
+        if layer not in kinds:
+            kinds.append(layer)
+    one_flops = sum(hip.useful_flops(lengths, hq, d, window=l.window) for l in kinds)
+    one_seconds = timed(kinds, 1, 3)
+    one_tflops = one_flops / one_seconds / 1e12
+    model = cpu_model()
+    sample = (f"full {workload.name} schedule ({len(workload.layers)} attention layers, T={T}) in fp32 on {threads} "
+              f"threads (physical cores of the affinity mask), median of {repeats} after 1 warm-up; band/short "
+              f"layers: {'reference pe_local_attention (oracle/_ref)' if kind == 'reference' else 'oracle C port'}; "
+              f"global layers longer than 128: per-segment torch SDPA. 1-thread: one layer of each kind "
+              f"({len(kinds)}), median of 3")
+    log(f"cpu baseline ({kind}, {threads} threads, {model}): {seconds * 1e3:.1f} ms/step -> "
+        f"{flops / seconds / 1e12:.3f} TFLOP/s; 1 thread {one_tflops:.4f} TFLOP/s")
     return {"value": round(flops / seconds / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": kind,
-            "sample": sample, "ms_per_step": round(seconds * 1e3, 2)}
+            "sample": sample, "ms_per_step": round(seconds * 1e3, 2), "repeats": repeats, "cpu_model": model,
+            "nproc": os.cpu_count(), "one_thread": {"value": round(one_tflops, 5), "unit": "TFLOP/s",
+                                                    "ms_per_sample": round(one_seconds * 1e3, 2),
+                                                    "layers": len(kinds)}}
 
 
 def copy_calibration(steps: int) -> int:

@@ -119,7 +119,10 @@ int pe_varlen_attn_fwd(const pe_attn_args *args, void *workspace, size_t workspa
    of them) or time one kernel. A plan is valid for arguments with the same cu_seqlens
    contents, n_seq, total_tokens, max_seqlen, head counts, window, causal and short_max.
    pe_attn_plan: build the cost-ordered (segment, query tile) list of the tiled kernel into
-     the workspace (no-op when no segment can exceed short_max).
+     the workspace (no-op when no segment can exceed short_max). The workspace starts with two
+     int32 words: the entries written and the entries needed. They differ only when the
+     arguments break the caller contract that sized the list (cu_seqlens decreasing or past
+     total_tokens); segments longer than max_seqlen (keys: max_seqlen_k) take no entry.
    pe_attn_short_fwd: the short kernel over segments with length <= short_max (no-op for 0).
    pe_attn_tiled_fwd: the tiled kernel over a planned workspace. */
 int pe_attn_plan(const pe_attn_args *args, void *workspace, size_t workspace_bytes, hipStream_t stream);

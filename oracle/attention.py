@@ -117,27 +117,50 @@ def sampled_rows_attention(q, k, v, cu_seqlens, rows, *, scale: float, window=(-
     """The oracle for selected token rows only (every head), float64 ``[len(rows), Hq, D]``.
 
     Each row needs only its own query against its segment's keys, so full-size outputs can be
-    checked on a sample at O(rows * L * D) cost."""
+    checked on a sample at O(rows * L * D) cost. The sampled rows of one segment are scored
+    together against the keys their windows span (kv head h // (Hq / Hkv) serves query head h)."""
     cu = np.asarray(cu_seqlens, dtype=np.int64)
+    rows = np.asarray(rows, dtype=np.int64)
     q = np.asarray(q)
-    hq, hkv = q.shape[1], k.shape[1]
+    hq, hkv, d = q.shape[1], k.shape[1], q.shape[2]
     group = hq // hkv
-    out = np.empty((len(rows), hq, q.shape[2]), dtype=np.float64)
-    seg_of = np.searchsorted(cu, np.asarray(rows), side="right") - 1
+    out = np.empty((len(rows), hq, d), dtype=np.float64)
+    seg_of = np.searchsorted(cu, rows, side="right") - 1
     left, right = window
     right = 0 if causal else right
-    for n, (row, s) in enumerate(zip(rows, seg_of)):
+    bounded = left >= 0 and right >= 0
+    for s in np.unique(seg_of):
         a, b = int(cu[s]), int(cu[s + 1])
-        i = int(row) - a
-        lo = a if left < 0 else max(a, a + i - left)
-        hi = b if right < 0 else min(b, a + i + right + 1)
-        kk = np.repeat(np.asarray(k[lo:hi], dtype=np.float64), group, axis=1)
-        vv = np.repeat(np.asarray(v[lo:hi], dtype=np.float64), group, axis=1)
-        sc = np.einsum("hd,khd->hk", np.asarray(q[row], dtype=np.float64), kk) * scale
-        sc -= sc.max(axis=-1, keepdims=True)
-        p = np.exp(sc)
-        p /= p.sum(axis=-1, keepdims=True)
-        out[n] = np.einsum("hk,khd->hd", p, vv)
+        members = np.nonzero(seg_of == s)[0]
+        members = members[np.argsort(rows[members], kind="stable")]
+        # rows of a bounded window are scored in clusters, so a cluster spans few keys
+        if bounded:
+            cut = np.nonzero(np.diff(rows[members]) > 64)[0] + 1
+            chunks = np.split(members, cut)
+        else:
+            chunks = [members]
+        for sel in chunks:
+            pos = rows[sel] - a
+            lo = 0 if left < 0 else max(0, int(pos.min()) - left)
+            hi = b - a if right < 0 else min(b - a, int(pos.max()) + right + 1)
+            # [hkv, keys, d] operands; queries [hkv, rows * group, d]
+            kk = np.asarray(k[a + lo:a + hi], dtype=np.float64).transpose(1, 0, 2)
+            vv = np.asarray(v[a + lo:a + hi], dtype=np.float64).transpose(1, 0, 2)
+            qq = np.asarray(q[rows[sel]], dtype=np.float64).reshape(len(sel), hkv, group, d)
+            qq = qq.transpose(1, 0, 2, 3).reshape(hkv, len(sel) * group, d)
+            sc = (qq @ kk.transpose(0, 2, 1)).reshape(hkv, len(sel), group, hi - lo) * scale
+            delta = pos[:, None] - np.arange(lo, hi)[None, :]
+            ok = np.ones(delta.shape, dtype=bool)
+            if left >= 0:
+                ok &= delta <= left
+            if right >= 0:
+                ok &= delta >= -right
+            sc = np.where(ok[None, :, None, :], sc, -np.inf)
+            sc -= sc.max(axis=-1, keepdims=True)
+            p = np.exp(sc)
+            p /= p.sum(axis=-1, keepdims=True)
+            o = p.reshape(hkv, len(sel) * group, hi - lo) @ vv  # [hkv, rows * group, d]
+            out[sel] = o.reshape(hkv, len(sel), group, d).transpose(1, 0, 2, 3).reshape(len(sel), hq, d)
     return out
 
 

@@ -246,9 +246,10 @@ int launch_tiled(const AttnParams &p, int d, int g, bool gate, int64_t cap, hipS
     return PE_ATTN_EUNSUPPORTED;
 }
 
-constexpr size_t kWorkspaceHeader = 256;  // the entry count lives here, list follows aligned
+constexpr size_t kWorkspaceHeader = 256;  // the entry counts live here, list follows aligned
 
-// Workspace layout: [0, 256) header (int32 entry count), then the (segment, tile) list.
+// Workspace layout: [0, 256) header (int32 entries written, int32 entries needed), then the
+// (segment, tile) list.
 struct Plan {
     int sm, g, bm, strip;
     int64_t cap;
@@ -321,8 +322,9 @@ int pe_attn_plan(const pe_attn_args *a, void *workspace, size_t workspace_bytes,
     int2 *work = reinterpret_cast<int2 *>(static_cast<char *>(workspace) + kWorkspaceHeader);
     const int wr = a->causal ? 0 : a->window_right;
     hipLaunchKernelGGL(pe::plan_kernel, dim3(1), dim3(1024), 0, stream, a->cu_seqlens,
-                       a->cu_seqlens_k ? a->cu_seqlens_k : a->cu_seqlens, a->n_seq, plan.sm, plan.bm, plan.strip,
-                       a->window_left, wr, a->head_dim > 64 ? 1 : 0, work, count, (int)plan.cap);
+                       a->cu_seqlens_k ? a->cu_seqlens_k : a->cu_seqlens, a->n_seq, plan.sm, a->max_seqlen,
+                       a->cu_seqlens_k ? a->max_seqlen_k : a->max_seqlen, plan.bm, plan.strip, a->window_left, wr,
+                       a->head_dim > 64 ? 1 : 0, work, count, (int)plan.cap);
     return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
 }
 

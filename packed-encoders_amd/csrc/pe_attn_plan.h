@@ -60,13 +60,21 @@ constexpr int kWaveQueue = 2048;
 
 // One entry per strip of `strip` consecutive query tiles of `bm` rows: (segment, first tile).
 // Segment s has cu[s + 1] - cu[s] query rows and cuk[s + 1] - cuk[s] keys (cuk = cu when the
-// two share boundaries); it is the short kernel's when both fit short_max. Pass 1 counts
-// entries per cost bucket, pass 2 reserves contiguous runs and writes them; both passes plan
-// each segment the same way (serially or by a wave), and a run's reservation is the same in
-// either.
+// two share boundaries); it is the short kernel's when both fit short_max. A segment longer
+// than the caller's max_seqlen (or whose keys exceed max_seqlen_k) breaks the contract the
+// host sized the list and the kernels' 32-bit offsets by: it takes no entry (the tiled
+// kernels would skip it anyway), so it can never push a valid segment's strips out of the
+// list. Pass 1 counts entries per cost bucket, pass 2 reserves contiguous runs and writes
+// them; both passes plan each segment the same way (serially or by a wave), and a run's
+// reservation is the same in either.
+//
+// count[0] receives the number of entries written, min(needed, cap); count[1] the number
+// needed. They differ only when the caller's sizes break the contract that sized cap
+// (cu_seqlens decreasing, or past total_tokens): the excess entries are then dropped, and
+// count[1] > count[0] records it where a caller can read it.
 __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int32_t *cuk, int n_seq, int short_max,
-                                                    int bm, int strip, int wl, int wr, int group, int2 *work,
-                                                    int32_t *count, int cap) {
+                                                    int max_seqlen, int max_seqlen_k, int bm, int strip, int wl,
+                                                    int wr, int group, int2 *work, int32_t *count, int cap) {
     __shared__ int cnt[64];
     __shared__ int off[64];
     __shared__ int3 queue[kWaveQueue];  // (segment, query rows, keys)
@@ -82,6 +90,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
         Lk = cuk[seg + 1] - cuk[seg];
         nq = (L + bm - 1) / bm;
         ns = (nq + strip - 1) / strip;
+        if (L < 0 || Lk < 0 || L > max_seqlen || Lk > max_seqlen_k) return false;  // outside the contract
         return max(L, Lk) > short_max;  // the tiled kernel's
     };
     for (int seg = tid; seg < n_seq; seg += blockDim.x) {
@@ -179,7 +188,8 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
             off[b] = run;
             run += cnt[b];
         }
-        *count = min(run, cap);
+        count[0] = min(run, cap);
+        count[1] = run;
     }
     __syncthreads();
     for (int seg = tid; seg < n_seq; seg += blockDim.x) serial_segment(seg, true);

@@ -331,12 +331,20 @@ def packed_short_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, 
 
 
 def select_packed_short_attention_config(max_seqlen: int, head_dim: int = 64) -> dict[str, int]:
-    """The short kernel's static launch choice for ``max_seqlen`` in JSON-friendly form (the
-    reference's triton_packed_attention.py:40-42; the fields describe this kernel's tiles)."""
+    """The short kernel's static launch choice for ``max_seqlen`` in JSON-friendly form.
+
+    Same keys as the reference's table (triton_packed_attention.py:22-42): ``block_m`` query
+    rows per wave, ``block_n`` keys staged per pass (the whole segment: the kernel holds up to
+    ``key_capacity`` keys in LDS at once), ``num_warps`` waves per workgroup (64 lanes each) and
+    ``num_stages`` staging passes (one: every load is issued before a single wait). The extra
+    keys describe this kernel's tiles. Like the reference, any ``max_seqlen`` gets an answer:
+    lengths past 128 report the 128-key shape, the largest the short kernel has (such batches
+    run the tiled kernel for their longer segments)."""
+    smax = min(max(int(max_seqlen), 1), 128)
     out = (ctypes.c_int32 * 4)()
-    _lib.check(_lib.library().pe_attn_short_config(int(max_seqlen), int(head_dim), out),
-               "pe_attn_short_config")
-    return {"block_m": out[0], "key_capacity": out[1], "heads_per_workgroup": out[2], "num_waves": out[3]}
+    _lib.check(_lib.library().pe_attn_short_config(smax, int(head_dim), out), "pe_attn_short_config")
+    return {"block_m": out[0], "block_n": out[1], "num_warps": out[3], "num_stages": 1,
+            "key_capacity": out[1], "heads_per_workgroup": out[2], "num_waves": out[3]}
 
 
 def useful_flops(lengths, n_heads_q: int, head_dim: int, *, window: tuple[int, int] = (-1, -1),

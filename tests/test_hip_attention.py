@@ -225,26 +225,55 @@ def test_rows_beyond_last_boundary_and_empty_segments_untouched(pe):
         _assert_parity(out, want, cu.cpu())
 
 
-@pytest.mark.parametrize("d", [64, 256])
-def test_segment_longer_than_max_seqlen_is_skipped(pe, d):
-    """max_seqlen sizes the kernels' 32-bit offsets; a segment longer than the caller's bound
-    breaches that contract and is left unwritten instead of being addressed, while the other
-    segments of the call are computed as usual."""
+@pytest.mark.parametrize("lengths,max_seqlen,skipped", [([100, 300, 150], 200, (100, 400)),
+                                                         ([300, 129, 129], 200, (0, 300))],
+                         ids=["middle", "evicts"])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_segment_longer_than_max_seqlen_is_skipped(pe, d, lengths, max_seqlen, skipped):
+    """max_seqlen sizes the kernels' 32-bit offsets and the plan's list; a segment longer than
+    the caller's bound breaches that contract and is left unwritten instead of being
+    addressed, while the other segments of the call are computed as usual. In the "evicts"
+    case the over-long segment alone would need more list entries than the capacity sized
+    from max_seqlen (3 tiles of 128 rows where the list holds 6 for all three segments): it
+    must take none, so no tile of a valid segment is dropped."""
     from packed_encoders_amd import _lib
 
-    announce(f"segment longer than max_seqlen d={d}")
-    lengths = [100, 300, 150]
-    q, k, v, cu, _ = _inputs(lengths, hq=4, hkv=4 if d == 64 else 1, d=d, seed=61)
+    announce(f"segment longer than max_seqlen d={d} lengths={lengths}")
+    q, k, v, cu, _ = _inputs(lengths, hq=4, hkv=1 if d == 256 else 4, d=d, seed=61)
     qd, kd, vd, cud = _dev(q, k, v, cu)
-    out = _launch(_lib.library(), qd, kd, vd, cud, 200, (-1, -1), False)
-    assert torch.all(out[100:400] == 3.0)
+    out = _launch(_lib.library(), qd, kd, vd, cud, max_seqlen, (-1, -1), False)
+    a, b = skipped
+    assert torch.all(out[a:b] == 3.0)
     want = _oracle(q, k, v, cu, scale=0.125)
     keep = torch.ones(sum(lengths), dtype=torch.bool)
-    keep[100:400] = False
+    keep[a:b] = False
     idx = keep.nonzero().flatten()
     got = out.float().cpu()[idx]
-    sub_cu = torch.tensor([0, 100, 250], dtype=torch.int32)
+    kept = [n for n in lengths if n <= max_seqlen]
+    sub_cu = torch.tensor([0, *np.cumsum(kept).tolist()], dtype=torch.int32)
     _assert_parity(got, want[idx.numpy()], sub_cu)
+
+
+def test_plan_reports_entries_written_and_needed(pe):
+    """The plan's header holds the entries it wrote and the entries it needed; with arguments
+    inside the contract (here an over-long segment that takes no entry) the two are equal."""
+    from packed_encoders_amd import _lib
+    from packed_encoders_amd.hip_attention import _args
+
+    announce("plan header counts")
+    lengths = [300, 129, 129, 40]
+    q, k, v, cu, _ = _inputs(lengths, hq=4, d=64, seed=62)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    out = torch.empty_like(qd)
+    a = _args(qd, kd, vd, out, cud, 200, 0.125, -1, -1, False, None, 64)
+    lib = _lib.library()
+    size = ctypes.c_size_t()
+    assert lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size)) == 0
+    ws = torch.zeros(size.value, dtype=torch.uint8, device="cuda")
+    assert lib.pe_attn_plan(ctypes.byref(a), ws.data_ptr(), size.value, torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    written, needed = ws[:8].view(torch.int32).tolist()
+    assert written == needed == 4  # two 129-row segments of two 128-row tiles; 300 and 40 take none
 
 
 def test_workspace_too_small_is_reported(pe):

@@ -159,8 +159,15 @@ def test_short_config_table(lib):
 
 
 def test_python_config_mirror(pe):
+    """The reference's keys (its dispatch bench reads config['block_n']) plus this kernel's own;
+    any length gets an answer, past 128 the largest shape."""
     cfg = pe.select_packed_short_attention_config(100)
-    assert cfg == {"block_m": 32, "key_capacity": 128, "heads_per_workgroup": 2, "num_waves": 4}
+    assert cfg == {"block_m": 32, "block_n": 128, "num_warps": 4, "num_stages": 1, "key_capacity": 128,
+                   "heads_per_workgroup": 2, "num_waves": 4}
+    assert {"block_m", "block_n", "num_warps", "num_stages"} <= set(pe.select_packed_short_attention_config(20))
+    assert pe.select_packed_short_attention_config(20)["block_n"] == 32
+    assert pe.select_packed_short_attention_config(4096) == pe.select_packed_short_attention_config(128)
+    assert pe.select_packed_short_attention_config(0)["block_n"] == 32
 
 
 def _rope_args(**kw):

@@ -110,18 +110,23 @@ def test_packed_forward_hip_matches_dense_fallback(pe):
 
 
 def test_packed_graph_runner_replays_match_eager(pe):
+    """Graph replays equal eager execution (and each other, bit for bit), and match the
+    Hugging Face forward of the same weights in fp32 at the bar of the pack() test."""
     announce("packed graph runner")
-    model = make_model().cuda().to(torch.bfloat16)
+    ref = make_model().cuda()
+    model = copy.deepcopy(ref).to(torch.bfloat16)
     config = pe.GraphConfig(max_batch=8, max_seq=512, pad_to=64, warmup=2)
     pe.pack(model, attention_backend="hip", cuda_graph=config, validate=False)
     engine = pe.get_engine(model)
     from packed_encoders_amd import forward
 
-    batches = []
+    batches, hf = [], []
     for lengths, seed in (([300, 100, 37], 5), ([37, 300, 90], 6), ([200, 200, 27], 7)):
         ids, mask = batch(lengths, seed=seed)
         flat, _, cu, max_seqlen, positions = forward.unpad(ids, mask)
         batches.append(pe.PackedBatch(flat, cu, max_seqlen, positions))
+        with torch.no_grad():
+            hf.append(ref(input_ids=ids, attention_mask=mask).last_hidden_state[mask.bool()])
     # same (M bucket, N) for all three; max_seqlen differs for the third
     with torch.no_grad():
         eager = []
@@ -140,6 +145,8 @@ def test_packed_graph_runner_replays_match_eager(pe):
                 assert cos.min() >= 0.999, (rep, i, cos.min())
                 if first[i] is None:
                     first[i] = got
+                    fp32 = token_cosine(got, hf[i])
+                    assert fp32.min() >= 0.995 and fp32.mean() >= 0.999, (i, fp32.min(), fp32.mean())
                 else:
                     assert torch.equal(got, first[i]), f"replay {rep} of batch {i} is not deterministic"
                 _ = torch.randn(1000, device="cuda").sum()  # unrelated eager work between replays

@@ -166,13 +166,16 @@ def test_oracle_matches_torch_sdpa_per_segment():
 
 
 def test_sampled_rows_match_full_oracle():
+    """Sampled rows (unsorted, repeated, in clusters further apart than a window) equal the
+    full oracle's rows for global, banded, asymmetric and causal attention with GQA."""
     rng = np.random.default_rng(8)
-    lengths = [40, 3, 90]
+    lengths = [40, 3, 90, 300]
     T = sum(lengths)
     q, k, v = _rand(rng, T, 4, 16), _rand(rng, T, 2, 16), _rand(rng, T, 2, 16)
     cu = _cu(lengths)
-    rows = [0, 39, 40, 42, 43, 100, 132]
-    for window, causal in (((-1, -1), False), ((5, 5), False), ((-1, -1), True)):
+    rows = [132, 0, 39, 40, 42, 43, 100, 133, 140, 431, 300, 299, 200, 140]
+    for window, causal in (((-1, -1), False), ((5, 5), False), ((64, 64), False), ((3, 70), False),
+                           ((-1, -1), True), ((20, -1), True)):
         full = oa.packed_attention(q, k, v, cu, scale=0.25, window=window, causal=causal)
         part = oa.sampled_rows_attention(q, k, v, cu, rows, scale=0.25, window=window, causal=causal)
         np.testing.assert_allclose(part, full[rows], atol=1e-12)
