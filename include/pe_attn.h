@@ -6,7 +6,8 @@
  * pointers and sizes, never throws, and returns 0 or a negative PE_ATTN_E* status. Kernels are
  * launched on the caller's stream with no host synchronisation and no device-to-host reads,
  * so every entry point is safe inside HIP graph capture. The library allocates nothing: the
- * one entry point that needs scratch memory takes a caller workspace.
+ * entry points that need scratch memory take a caller workspace, or (pe_varlen_attn_fwd_noalloc)
+ * use a fixed array in device memory.
  *
  * Semantics (identical for every entry point):
  *   For each segment s with start = cu_seqlens[s], length L = cu_seqlens[s+1] - start, each
@@ -36,13 +37,14 @@
 extern "C" {
 #endif
 
-#define PE_ATTN_ABI_VERSION 4
+#define PE_ATTN_ABI_VERSION 5
 
 #define PE_ATTN_OK 0
 #define PE_ATTN_EINVAL (-1)       /* malformed arguments (maps to ValueError) */
 #define PE_ATTN_EUNSUPPORTED (-2) /* well-formed but outside the kernels' envelope */
 #define PE_ATTN_EWORKSPACE (-3)   /* workspace missing or too small */
 #define PE_ATTN_ELAUNCH (-4)      /* a kernel launch failed (maps to RuntimeError) */
+#define PE_ATTN_ESCRATCH (-5)     /* the call needs more than the library's static scratch */
 
 #define PE_ATTN_DTYPE_BF16 1
 
@@ -113,6 +115,18 @@ int pe_attn_workspace_size(const pe_attn_args *args, size_t *bytes);
    gate (packed_encoders/_kernels/hybrid.py:197-219) included. */
 int pe_varlen_attn_fwd(const pe_attn_args *args, void *workspace, size_t workspace_bytes,
                        hipStream_t stream);
+
+/* pe_varlen_attn_fwd with its workspace in a static device array of PE_ATTN_STATIC_SCRATCH_BYTES
+   (one copy per GPU, held until the process ends) instead of a caller allocation: for callers
+   that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+   forbid hipMalloc). No counterpart in the reference. It calls no allocating routine; its first
+   call on a device looks the array's device address up once (hipGetSymbolAddress).
+   Returns PE_ATTN_ESCRATCH, launching nothing, when pe_attn_workspace_size exceeds the array
+   (at 1 MiB: about 131,000 (segment, query tile) entries). Every call on one GPU shares that
+   GPU's array: calls that overlap on one GPU (other streams, other threads) race and must be
+   serialised by the caller. */
+#define PE_ATTN_STATIC_SCRATCH_BYTES (1u << 20)
+int pe_varlen_attn_fwd_noalloc(const pe_attn_args *args, hipStream_t stream);
 
 /* The three stages pe_varlen_attn_fwd runs, for callers that reuse one plan across calls
    (the 22 layers of a packed forward share cu_seqlens: one plan per window kind serves all

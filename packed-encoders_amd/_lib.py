@@ -12,16 +12,18 @@ from pathlib import Path
 
 from ._build import LIBRARY
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 DTYPE_BF16 = 1
 
-OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH = 0, -1, -2, -3, -4
+OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, ESCRATCH = 0, -1, -2, -3, -4, -5
+STATIC_SCRATCH_BYTES = 1 << 20  # PE_ATTN_STATIC_SCRATCH_BYTES
 
 EXPORTED = (
     "pe_attn_abi_version",
     "pe_attn_strerror",
     "pe_attn_workspace_size",
     "pe_varlen_attn_fwd",
+    "pe_varlen_attn_fwd_noalloc",
     "pe_attn_plan",
     "pe_attn_short_fwd",
     "pe_attn_tiled_fwd",
@@ -111,6 +113,8 @@ def library(path: str | None = None) -> ctypes.CDLL:
     lib.pe_attn_workspace_size.argtypes = [ctypes.POINTER(AttnArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.pe_varlen_attn_fwd.restype = ctypes.c_int
     lib.pe_varlen_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.pe_varlen_attn_fwd_noalloc.restype = ctypes.c_int
+    lib.pe_varlen_attn_fwd_noalloc.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p]
     lib.pe_attn_plan.restype = ctypes.c_int
     lib.pe_attn_plan.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.pe_attn_short_fwd.restype = ctypes.c_int
@@ -138,6 +142,6 @@ def check(status: int, what: str) -> None:
     if status == OK:
         return
     message = f"{what}: {strerror(status)} ({status})"
-    if status in (EINVAL, EUNSUPPORTED, EWORKSPACE):
+    if status in (EINVAL, EUNSUPPORTED, EWORKSPACE, ESCRATCH):
         raise ValueError(message)
     raise RuntimeError(message)

@@ -9,6 +9,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 
 #include "pe_attn_device.h"
 #include "pe_attn_plan.h"
@@ -17,9 +18,35 @@
 #include "pe_attn_tiled_wide16.h"
 #include "pe_rope.h"
 
+namespace pe {
+// Workspace of pe_varlen_attn_fwd_noalloc: one copy per GPU, in device memory for the life of
+// the process. In host code `scratch` names a host-side stand-in, never the device array: the
+// array is reached only through the address hipGetSymbolAddress returns for the current
+// device, kept per device (static_scratch below).
+__device__ __align__(256) unsigned char scratch[PE_ATTN_STATIC_SCRATCH_BYTES];
+}  // namespace pe
+
 namespace {
 
 using pe::AttnParams;
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_lock;
+void *scratch_ptr[kMaxDevices];
+
+// The current device's address of pe::scratch, looked up once per device.
+int static_scratch(void **ptr) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return PE_ATTN_ELAUNCH;
+    std::lock_guard<std::mutex> guard(scratch_lock);
+    if (!scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(pe::scratch)) != hipSuccess || !p) return PE_ATTN_ELAUNCH;
+        scratch_ptr[dev] = p;
+    }
+    *ptr = scratch_ptr[dev];
+    return PE_ATTN_OK;
+}
 
 constexpr int kDefaultShortMax = 64;  // gfx950 default routing boundary (head_dim <= 128)
 constexpr int kMaxStrip = 64;         // query tiles per tiled-kernel workgroup, at most
@@ -296,6 +323,7 @@ const char *pe_attn_strerror(int status) {
         case PE_ATTN_EUNSUPPORTED: return "unsupported configuration";
         case PE_ATTN_EWORKSPACE: return "workspace missing or too small";
         case PE_ATTN_ELAUNCH: return "kernel launch failed";
+        case PE_ATTN_ESCRATCH: return "needs more than the static scratch (PE_ATTN_STATIC_SCRATCH_BYTES)";
         default: return "unknown status";
     }
 }
@@ -359,6 +387,18 @@ int pe_varlen_attn_fwd(const pe_attn_args *a, void *workspace, size_t workspace_
     if ((rc = pe_attn_short_fwd(a, stream))) return rc;
     if ((rc = pe_attn_plan(a, workspace, workspace_bytes, stream))) return rc;
     return pe_attn_tiled_fwd(a, workspace, workspace_bytes, stream);
+}
+
+int pe_varlen_attn_fwd_noalloc(const pe_attn_args *a, hipStream_t stream) {
+    size_t need = 0;
+    int rc = pe_attn_workspace_size(a, &need);
+    if (rc) return rc;
+    if (need > PE_ATTN_STATIC_SCRATCH_BYTES) return PE_ATTN_ESCRATCH;
+    void *ws = nullptr;
+    if (need > 0 && (rc = static_scratch(&ws))) return rc;
+    // Nothing in the workspace needs clearing: the plan writes the entry counts before the
+    // tiled kernel reads them, and entries only up to that count.
+    return pe_varlen_attn_fwd(a, ws, need, stream);
 }
 
 int pe_packed_short_attn_fwd(const pe_attn_args *a, hipStream_t stream) {

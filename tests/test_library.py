@@ -54,7 +54,7 @@ def test_library_holds_gfx950_code():
 
 
 def test_abi_version_and_status_text(lib):
-    assert lib.pe_attn_abi_version() == 4
+    assert lib.pe_attn_abi_version() == 5
     assert lib.pe_attn_strerror(0) == b"ok"
     assert lib.pe_attn_strerror(-3) == b"workspace missing or too small"
     assert lib.pe_attn_strerror(-99) == b"unknown status"
@@ -202,3 +202,19 @@ def test_rope_missing_pointers_misaligned_strides_and_empty_input(lib):
     assert lib.pe_rope_qkv_fwd(ctypes.byref(a), None) == -1  # rows narrower than 3HD
     a = _rope_args(qkv=p + 2, cos=p, sin=p, q_out=p, k_out=p)
     assert lib.pe_rope_qkv_fwd(ctypes.byref(a), None) == -1  # misaligned base
+
+
+def test_noalloc_entry_point_rejects_calls_past_its_static_scratch(lib):
+    """pe_varlen_attn_fwd_noalloc holds the plan list in a fixed device array: a call whose
+    workspace would exceed it is refused with PE_ATTN_ESCRATCH before anything is launched or
+    any device pointer is read (here there are none)."""
+    from packed_encoders_amd import _lib
+
+    big = _args(n_seq=200000, total_tokens=1 << 27, max_seqlen=4096, short_max=0)
+    rc, size = _ws(lib, big)
+    assert rc == 0 and size > _lib.STATIC_SCRATCH_BYTES
+    assert lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(big), None) == _lib.ESCRATCH
+    assert lib.pe_attn_strerror(_lib.ESCRATCH).startswith(b"needs more than the static scratch")
+    # malformed arguments are still reported as such
+    assert lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(_args(head_dim=96)), None) == -2
+    assert lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(_args(n_seq=0, total_tokens=0)), None) == 0
