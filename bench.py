@@ -126,6 +126,8 @@ def kernel_instance(stage, workload, layer, short_max):
     flags = f"{str(layer.gate).lower()}, {str(win).lower()}"
     if d == 256:
         return f"pe::wide16_attn_kernel<{d}, 4, {g}, {ns}, {flags}>"  # four waves per workgroup
+    if d == 64 and not win:
+        return f"pe::global64_attn_kernel<{g}, {str(layer.gate).lower()}>"
     name = "tiled_attn_kernel" if d == 64 else "wide_attn_kernel"
     return f"pe::{name}<{d}, {g}, {bn}, {ns}, {flags}>"
 

@@ -12,6 +12,7 @@
 #include <mutex>
 
 #include "pe_attn_device.h"
+#include "pe_attn_global64.h"
 #include "pe_attn_plan.h"
 #include "pe_attn_short.h"
 #include "pe_attn_tiled.h"
@@ -224,7 +225,15 @@ struct TiledShape {
 };
 
 // Query rows per tiled-kernel tile for g query heads per workgroup (the plan's tile height).
-int tile_rows(int head_dim, int g) { return head_dim == 256 ? 16 * kWide16Waves / g : 32 * (4 / g); }
+// Global head_dim 64 calls run global64_attn_kernel, whose waves hold 64 query rows.
+bool global64(const pe_attn_args *a) {
+    return a->head_dim == 64 && a->window_left < 0 && a->window_right < 0 && !a->causal;
+}
+
+int tile_rows(const pe_attn_args *a, int g) {
+    if (a->head_dim == 256) return 16 * kWide16Waves / g;
+    return (global64(a) ? 64 : 32) * (4 / g);
+}
 
 template <int D, int G, bool GATE, bool WIN>
 int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
@@ -240,7 +249,9 @@ int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
     const int64_t blocks = (D > 64 || WIN) ? (cap * p.hgroups + run - 1) / run * run : cap * p.hgroups;
     if (blocks <= 0) return PE_ATTN_OK;
     if (blocks > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
-    if constexpr (D == 64)
+    if constexpr (D == 64 && !WIN)
+        hipLaunchKernelGGL((pe::global64_attn_kernel<G, GATE>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    else if constexpr (D == 64)
         hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, NS, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0,
                            stream, p);
     else if constexpr (D == 256)
@@ -287,7 +298,7 @@ int prepare(const pe_attn_args *a, Plan *plan) {
     if (rc) return rc;
     plan->sm = effective_short_max(a);
     plan->g = heads_per_tile(a);
-    plan->bm = tile_rows(a->head_dim, plan->g);
+    plan->bm = tile_rows(a, plan->g);
     plan->strip = effective_strip(a);
     plan->cap = tile_capacity(a, plan->sm, plan->bm, plan->strip);
     if (plan->cap > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
@@ -334,7 +345,7 @@ int pe_attn_workspace_size(const pe_attn_args *a, size_t *bytes) {
     if (rc) return rc;
     const int sm = effective_short_max(a);
     const int g = heads_per_tile(a);
-    const int64_t cap = tile_capacity(a, sm, tile_rows(a->head_dim, g), effective_strip(a));
+    const int64_t cap = tile_capacity(a, sm, tile_rows(a, g), effective_strip(a));
     *bytes = cap > 0 ? kWorkspaceHeader + (size_t)cap * sizeof(int2) : 0;
     return PE_ATTN_OK;
 }

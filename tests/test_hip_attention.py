@@ -233,8 +233,8 @@ def test_segment_longer_than_max_seqlen_is_skipped(pe, d, lengths, max_seqlen, s
     """max_seqlen sizes the kernels' 32-bit offsets and the plan's list; a segment longer than
     the caller's bound breaches that contract and is left unwritten instead of being
     addressed, while the other segments of the call are computed as usual. In the "evicts"
-    case the over-long segment alone would need more list entries than the capacity sized
-    from max_seqlen (3 tiles of 128 rows where the list holds 6 for all three segments): it
+    case the list is sized from max_seqlen (for head_dim 128: 6 entries of 128-row tiles, for
+    head_dim 64's 256-row tiles: 3) and the over-long segment's tiles alone would fill it: it
     must take none, so no tile of a valid segment is dropped."""
     from packed_encoders_amd import _lib
 
@@ -273,7 +273,7 @@ def test_plan_reports_entries_written_and_needed(pe):
     assert lib.pe_attn_plan(ctypes.byref(a), ws.data_ptr(), size.value, torch.cuda.current_stream().cuda_stream) == 0
     torch.cuda.synchronize()
     written, needed = ws[:8].view(torch.int32).tolist()
-    assert written == needed == 4  # two 129-row segments of two 128-row tiles; 300 and 40 take none
+    assert written == needed == 2  # two 129-row segments of one 256-row tile; 300 and 40 take none
 
 
 def test_workspace_too_small_is_reported(pe):

@@ -83,12 +83,16 @@ def _ws(lib, a):
 
 
 def test_workspace_size_is_host_arithmetic(lib):
-    # 64 segments, max 2048: tiles of 128 rows; bound min(N*ceil(S/128), (T + N_long*127)/128)
+    # 64 segments, max 2048, global head_dim 64: tiles of 256 rows (four waves of 64);
+    # bound min(N*ceil(S/256), (T + N_long*255)/256)
     rc, size = _ws(lib, _args())
     assert rc == 0
     n_long = min(64, 32438 // 65)
-    cap = min(64 * 16, (32438 + n_long * 127) // 128)
+    cap = min(64 * 8, (32438 + n_long * 255) // 256)
     assert size == 256 + 8 * cap
+    # windowed head_dim 64: tiles of 128 rows (four waves of 32)
+    rc, size = _ws(lib, _args(window_left=64, window_right=64))
+    assert rc == 0 and size == 256 + 8 * min(64 * 16, (32438 + n_long * 127) // 128)
     # every segment fits the short kernel: no workspace
     rc, size = _ws(lib, _args(max_seqlen=64))
     assert rc == 0 and size == 0
@@ -100,10 +104,10 @@ def test_workspace_size_is_host_arithmetic(lib):
     rc, size = _ws(lib, _args(n_heads_q=8, n_heads_kv=2, head_dim=128, max_seqlen=512, n_seq=256, total_tokens=71104))
     assert rc == 0
     assert size == 256 + 8 * min(256 * 16, (71104 + 256 * 31) // 32)
-    # strips of 4 query tiles: min(N * ceil(ceil(S/128)/4), (tiles_by_tokens + N_long*3) // 4)
+    # strips of 4 query tiles: min(N * ceil(ceil(S/256)/4), (tiles_by_tokens + N_long*3) // 4)
     rc, size = _ws(lib, _args(strip=4))
-    tiles = (32438 + n_long * 127) // 128
-    assert rc == 0 and size == 256 + 8 * min(64 * 4, (tiles + n_long * 3) // 4)
+    tiles = (32438 + n_long * 255) // 256
+    assert rc == 0 and size == 256 + 8 * min(64 * 2, (tiles + n_long * 3) // 4)
 
 
 @pytest.mark.parametrize("field,value,status", [
