@@ -122,7 +122,7 @@ int pe_varlen_attn_fwd(const pe_attn_args *args, void *workspace, size_t workspa
    forbid hipMalloc). No counterpart in the reference. It calls no allocating routine; its first
    call on a device looks the array's device address up once (hipGetSymbolAddress).
    Returns PE_ATTN_ESCRATCH, launching nothing, when pe_attn_workspace_size exceeds the array
-   (at 1 MiB: about 131,000 (segment, query tile) entries). Every call on one GPU shares that
+   (at 1 MiB: about 65,000 (segment, query tile) entries). Every call on one GPU shares that
    GPU's array: calls that overlap on one GPU (other streams, other threads) race and must be
    serialised by the caller. */
 #define PE_ATTN_STATIC_SCRATCH_BYTES (1u << 20)

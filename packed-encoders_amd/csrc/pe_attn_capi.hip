@@ -287,7 +287,7 @@ int launch_tiled(const AttnParams &p, int d, int g, bool gate, int64_t cap, hipS
 constexpr size_t kWorkspaceHeader = 256;  // the entry counts live here, list follows aligned
 
 // Workspace layout: [0, 256) header (int32 entries written, int32 entries needed), then the
-// (segment, tile) list.
+// list of (segment, first query tile, query start, query rows) int4 entries.
 struct Plan {
     int sm, g, bm, strip;
     int64_t cap;
@@ -307,7 +307,7 @@ int prepare(const pe_attn_args *a, Plan *plan) {
 
 int check_workspace(const Plan &plan, const void *workspace, size_t bytes) {
     if (plan.cap > 0 && (!workspace || !aligned16(workspace) ||
-                         bytes < kWorkspaceHeader + (size_t)plan.cap * sizeof(int2)))
+                         bytes < kWorkspaceHeader + (size_t)plan.cap * sizeof(int4)))
         return PE_ATTN_EWORKSPACE;
     return PE_ATTN_OK;
 }
@@ -346,7 +346,7 @@ int pe_attn_workspace_size(const pe_attn_args *a, size_t *bytes) {
     const int sm = effective_short_max(a);
     const int g = heads_per_tile(a);
     const int64_t cap = tile_capacity(a, sm, tile_rows(a, g), effective_strip(a));
-    *bytes = cap > 0 ? kWorkspaceHeader + (size_t)cap * sizeof(int2) : 0;
+    *bytes = cap > 0 ? kWorkspaceHeader + (size_t)cap * sizeof(int4) : 0;
     return PE_ATTN_OK;
 }
 
@@ -358,7 +358,7 @@ int pe_attn_plan(const pe_attn_args *a, void *workspace, size_t workspace_bytes,
     rc = check_workspace(plan, workspace, workspace_bytes);
     if (rc) return rc;
     int32_t *count = static_cast<int32_t *>(workspace);
-    int2 *work = reinterpret_cast<int2 *>(static_cast<char *>(workspace) + kWorkspaceHeader);
+    int4 *work = reinterpret_cast<int4 *>(static_cast<char *>(workspace) + kWorkspaceHeader);
     const int wr = a->causal ? 0 : a->window_right;
     hipLaunchKernelGGL(pe::plan_kernel, dim3(1), dim3(1024), 0, stream, a->cu_seqlens,
                        a->cu_seqlens_k ? a->cu_seqlens_k : a->cu_seqlens, a->n_seq, plan.sm, a->max_seqlen,
@@ -385,7 +385,8 @@ int pe_attn_tiled_fwd(const pe_attn_args *a, const void *workspace, size_t works
     if (rc) return rc;
     AttnParams p = make_params(a, plan.sm);
     p.work_count = static_cast<const int32_t *>(workspace);
-    p.work = reinterpret_cast<const int2 *>(static_cast<const char *>(workspace) + kWorkspaceHeader);
+    p.work = reinterpret_cast<const int4 *>(static_cast<const char *>(workspace) + kWorkspaceHeader);
+    p.work_cap = (int)plan.cap;
     return launch_tiled(p, a->head_dim, plan.g, a->gate != nullptr, plan.cap, stream);
 }
 

@@ -45,9 +45,39 @@ struct AttnParams {
     int32_t hgroups; // head groups per work entry (tiled kernel)
     int32_t strip;   // query tiles per work entry (tiled kernel)
     float c;         // softmax_scale * log2(e)
-    const int2 *work;          // tiled kernel: (segment, q-tile) entries
-    const int32_t *work_count; // tiled kernel: number of valid entries
+    const int4 *work;          // tiled kernels: (segment, first q-tile, query start, query rows)
+    const int32_t *work_count; // tiled kernels: number of valid entries
+    int32_t work_cap;          // entries the workspace holds
 };
+
+// A tiled kernel's work item: the plan's (segment, first query tile, query start, query rows)
+// and the segment's keys. The entry is loaded together with the entry count, its index clamped
+// to the list's capacity so the read stays inside the workspace: the two loads overlap, and the
+// segment's bounds come with the entry instead of a further dependent read of cu_seqlens (keys
+// are read from cu_seqlens_k only when it differs from cu_seqlens). `valid` is false for an
+// index past the count or an entry planned for other arguments.
+struct WorkItem {
+    int seg, qt_first, start, L, kstart, Lk;
+    bool valid;
+};
+
+__device__ __forceinline__ WorkItem load_work(const AttnParams &p, int entry) {
+    const int count = p.work_count[0];
+    const int4 w = p.work[min(max(entry, 0), p.work_cap - 1)];
+    WorkItem it;
+    it.seg = w.x;
+    it.qt_first = w.y;
+    it.start = w.z;
+    it.L = w.w;
+    it.valid = entry >= 0 && entry < count && w.x >= 0 && w.x < p.n_seq && w.y >= 0 && p.strip >= 1;
+    it.kstart = w.z;
+    it.Lk = w.w;
+    if (p.cuk != p.cu && it.valid) {
+        it.kstart = p.cuk[w.x];
+        it.Lk = p.cuk[w.x + 1] - it.kstart;
+    }
+    return it;
+}
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));

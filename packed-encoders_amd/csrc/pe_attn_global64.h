@@ -71,18 +71,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     __shared__ __attribute__((aligned(16))) __bf16 ring[NS][2][TILE];
 
-    const int count = p.work_count[0];
     const int item = blockIdx.x;
     const int entry = item / p.hgroups;
     const int hg = item - entry * p.hgroups;
-    if (entry >= count) return;
-    const int2 w = p.work[entry];
-    const int seg = w.x, qt_first = w.y;
-    if (seg < 0 || seg >= p.n_seq || qt_first < 0 || p.strip < 1) return;  // a plan made for other arguments
-    const int start = p.cu[seg];
-    const int L = p.cu[seg + 1] - start;  // query rows
-    const int kstart = p.cuk[seg];
-    const int Lk = p.cuk[seg + 1] - kstart;  // keys (every row reads all of them)
+    const WorkItem wi = load_work(p, entry);
+    if (!wi.valid) return;
+    const int qt_first = wi.qt_first;
+    const int start = wi.start, L = wi.L;      // query rows
+    const int kstart = wi.kstart, Lk = wi.Lk;  // keys (every row reads all of them)
     // A segment longer than the caller's max_seqlen breaks the contract the host sized the
     // 32-bit buffer offsets by: its rows are left unwritten rather than addressed.
     if (L > p.max_seqlen || Lk > p.max_seqlen_k || Lk < 0) return;
@@ -288,16 +284,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             st0 = sum2(pb[1], 2, st0);
             st1 = sum2(pb[1], 3, st1);
         };
-        // Stale-maximum softmax of half x's scores s into pb: false (nothing added) when some
-        // row's probabilities pass the guard, else the sums are added to the row sums.
-        auto softmax_stale = [&](f32x16 &s, int x, bf16x8 (&pb)[2]) {
-            float st0, st1;
-            probs(s, x, pb, st0, st1);
-            if (wave_any(fmaxf(st0, st1) > kG64OverflowGuard)) return false;
-            ls[x][0] += st0;
-            ls[x][1] += st1;
-            return true;
-        };
         // The exact path, from half block `from` (2 b + x) of the stage's key tile to its end:
         // scores recomputed from the stage (blocks past the keys skipped, the straddling block
         // masked), the maximum raised to cover them, probabilities, P.V. It serves the segment's
@@ -345,41 +331,81 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             m[x] = pair_max(fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]))) * c2;
             nm[x] = -m[x];
         };
+        // Softmax check of a half block: false when some row's probabilities pass the guard
+        // (nothing added), else its sums are added to the row sums.
+        auto accept = [&](int x, float st0, float st1) {
+            if (wave_any(fmaxf(st0, st1) > kG64OverflowGuard)) return false;
+            ls[x][0] += st0;
+            ls[x][1] += st1;
+            return true;
+        };
         // A full key tile in the pipelined order, under the stale maximum. Returns 4 when done,
         // else the half block (2 b + x) whose softmax overflowed: it and everything after it are
-        // left to exact_from. On a query tile's first key tile (`first`) the maximum is seeded
-        // from block 0's scores before any probability is taken. (sched_barrier keeps the phases
-        // in this order; left free, the scheduler hoists every LDS read of the tile and runs out
-        // of registers.)
-        auto pipelined_tile = [&](const __bf16 *kt, const __bf16 *vt, bool first) -> int {
+        // left to exact_from. Each region between checks issues its MFMAs one at a time between
+        // groups of the independent softmax VALU work (sched_group_barrier: 0x008 MFMA, 0x002
+        // VALU, 0x100 LDS read), so the wave keeps the matrix core fed while it computes
+        // probabilities; sched_barrier fences the regions.
+        auto pipelined_tile = [&](const __bf16 *kt, const __bf16 *vt) -> int {
             bf16x8 k4[4], v4[2][2], pa[2], pbb[2];
+            float st0, st1;
+            // R0: S_A0, S_B0; softmax A0 under S_B0.
             load_k(kt, 0, k4);
             f32x16 sa = qk(k4, 0);
             f32x16 sb = qk(k4, 1);
-            if (first) {
-                seed_max(sa, 0);
-                seed_max(sb, 1);
+            probs(sa, 0, pa, st0, st1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (!softmax_stale(sa, 0, pa)) return 0;
+            if (!accept(0, st0, st1)) return 0;
             __builtin_amdgcn_sched_barrier(0);
+            // R1: S_A1, O_A += V0 P_A0; softmax B0 under them.
             load_k(kt, 1, k4);
-            sa = qk(k4, 0);
             load_v(vt, 0, v4);
+            sa = qk(k4, 0);
             pv(v4, pa, 0);
+            probs(sb, 1, pbb, st0, st1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
-            if (!softmax_stale(sb, 1, pbb)) return 1;
+            if (!accept(1, st0, st1)) return 1;
             __builtin_amdgcn_sched_barrier(0);
+            // R2: S_B1, O_B += V0 P_B0; softmax A1 under them.
             sb = qk(k4, 1);
             pv(v4, pbb, 1);
+            probs(sa, 0, pa, st0, st1);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
-            if (!softmax_stale(sa, 0, pa)) return 2;
+            if (!accept(0, st0, st1)) return 2;
             __builtin_amdgcn_sched_barrier(0);
+            // R3: O_A += V1 P_A1; softmax B1 under it.
             load_v(vt, 1, v4);
             pv(v4, pa, 0);
+            probs(sb, 1, pbb, st0, st1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
-            if (!softmax_stale(sb, 1, pbb)) return 3;
+            if (!accept(1, st0, st1)) return 3;
             __builtin_amdgcn_sched_barrier(0);
+            // R4: O_B += V1 P_B1.
             pv(v4, pbb, 1);
             return 4;
         };
@@ -390,7 +416,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
                 const __bf16 *kt = &ring[stage][0][0];
                 const __bf16 *vt = &ring[stage][1][0];
                 const int kt0 = t * BN;
-                const int from = kt0 + BN <= Lk ? pipelined_tile(kt, vt, t == 0) : 0;
+                int from = 0;
+                if (kt0 + BN <= Lk) {
+                    if (t == 0) {
+                        // First key tile: the stale maximum seeded from block 0's scores (8
+                        // MFMAs more per query tile; the pipelined schedule itself stays free of
+                        // branches).
+                        bf16x8 k4[4];
+                        load_k(kt, 0, k4);
+                        const f32x16 sa = qk(k4, 0);
+                        const f32x16 sb = qk(k4, 1);
+                        seed_max(sa, 0);
+                        seed_max(sb, 1);
+                    }
+                    from = pipelined_tile(kt, vt);
+                }
                 if (from < 4) exact_from(kt, vt, kt0, from);
             }
             end_step();

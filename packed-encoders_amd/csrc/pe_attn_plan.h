@@ -58,7 +58,9 @@ __device__ __forceinline__ int plan_bucket(int cost) {
 constexpr int kSerialStrips = 32;
 constexpr int kWaveQueue = 2048;
 
-// One entry per strip of `strip` consecutive query tiles of `bm` rows: (segment, first tile).
+// One entry per strip of `strip` consecutive query tiles of `bm` rows: (segment, first tile,
+// the segment's first query row, its query rows), so a kernel reads a work item's bounds with
+// the entry itself.
 // Segment s has cu[s + 1] - cu[s] query rows and cuk[s + 1] - cuk[s] keys (cuk = cu when the
 // two share boundaries); it is the short kernel's when both fit short_max. A segment longer
 // than the caller's max_seqlen (or whose keys exceed max_seqlen_k) breaks the contract the
@@ -74,10 +76,10 @@ constexpr int kWaveQueue = 2048;
 // count[1] > count[0] records it where a caller can read it.
 __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int32_t *cuk, int n_seq, int short_max,
                                                     int max_seqlen, int max_seqlen_k, int bm, int strip, int wl,
-                                                    int wr, int group, int2 *work, int32_t *count, int cap) {
+                                                    int wr, int group, int4 *work, int32_t *count, int cap) {
     __shared__ int cnt[64];
     __shared__ int off[64];
-    __shared__ int3 queue[kWaveQueue];  // (segment, query rows, keys)
+    __shared__ int4 queue[kWaveQueue];  // (segment, query rows, keys, query start)
     __shared__ int queued;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
         int L, Lk, nq, ns;
         if (strips_of(seg, L, Lk, nq, ns) && ns > kSerialStrips) {
             const int qi = atomicAdd(&queued, 1);
-            if (qi < kWaveQueue) queue[qi] = make_int3(seg, L, Lk);
+            if (qi < kWaveQueue) queue[qi] = make_int4(seg, L, Lk, cu[seg]);
         }
     }
     __syncthreads();
@@ -118,10 +120,12 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
             const int pos = atomicAdd(&off[b], ns);
             const bool rev =
                 plan_strip_cost(ns - 1, strip, nq, bm, L, Lk, wl, wr) > plan_strip_cost(0, strip, nq, bm, L, Lk, wl, wr);
+            const int start = cu[seg];
             for (int i = 0; i < ns; ++i)
-                if (pos + i < cap) work[pos + i] = make_int2(seg, (rev ? ns - 1 - i : i) * strip);
+                if (pos + i < cap) work[pos + i] = make_int4(seg, (rev ? ns - 1 - i : i) * strip, start, L);
             return;
         }
+        const int start = cu[seg];
         int s = 0;
         while (s < ns) {
             // A run of consecutive strips in one cost bucket gets one contiguous reservation.
@@ -133,15 +137,15 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
             } else {
                 const int pos = atomicAdd(&off[b], e - s);
                 for (int i = 0; i < e - s; ++i)
-                    if (pos + i < cap) work[pos + i] = make_int2(seg, (s + i) * strip);
+                    if (pos + i < cap) work[pos + i] = make_int4(seg, (s + i) * strip, start, L);
             }
             s = e;
         }
     };
     // A wave plans segment seg (wave-uniform), lane i taking strips i, i + 64, ...: runs of
     // equal buckets within each 64-strip chunk are found with a ballot, one atomic per run.
-    auto wave_segment = [&](int3 q, bool place) {
-        const int seg = q.x, L = q.y, Lk = q.z;
+    auto wave_segment = [&](int4 q, bool place) {
+        const int seg = q.x, L = q.y, Lk = q.z, row0 = q.w;
         const int nq = (L + bm - 1) / bm;
         const int ns = (nq + strip - 1) / strip;
         if (group) {
@@ -157,7 +161,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
             const bool rev =
                 plan_strip_cost(ns - 1, strip, nq, bm, L, Lk, wl, wr) > plan_strip_cost(0, strip, nq, bm, L, Lk, wl, wr);
             for (int i = lane; i < ns; i += 64)
-                if (pos + i < cap) work[pos + i] = make_int2(seg, (rev ? ns - 1 - i : i) * strip);
+                if (pos + i < cap) work[pos + i] = make_int4(seg, (rev ? ns - 1 - i : i) * strip, row0, L);
             return;
         }
         for (int s0 = 0; s0 < ns; s0 += 64) {
@@ -175,7 +179,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
             const uint64_t upto = starts & (lane == 63 ? ~0ull : (2ull << lane) - 1);
             const int rs = 63 - __clzll((long long)upto);  // this lane's run start
             const int p0 = __shfl(pos, rs);
-            if (valid && p0 + (lane - rs) < cap) work[p0 + lane - rs] = make_int2(seg, s * strip);
+            if (valid && p0 + (lane - rs) < cap) work[p0 + lane - rs] = make_int4(seg, s * strip, row0, L);
         }
     };
 

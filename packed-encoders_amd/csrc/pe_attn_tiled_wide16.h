@@ -67,14 +67,11 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
     const int item = ((j / rh) * 8 + (int)(blockIdx.x & 7)) * rh + j % rh;
     const int entry = item / p.hgroups;
     const int hg = item - entry * p.hgroups;
-    if (entry >= *p.work_count) return;
-    const int2 w = p.work[entry];
-    const int seg = w.x, qt_first = w.y;
-    if (seg < 0 || seg >= p.n_seq || qt_first < 0 || p.strip < 1) return;  // a plan made for other arguments
-    const int start = p.cu[seg];
-    const int L = p.cu[seg + 1] - start;  // query rows
-    const int kstart = p.cuk[seg];
-    const int Lk = p.cuk[seg + 1] - kstart;  // keys
+    const WorkItem wi = load_work(p, entry);
+    if (!wi.valid) return;
+    const int qt_first = wi.qt_first;
+    const int start = wi.start, L = wi.L;      // query rows
+    const int kstart = wi.kstart, Lk = wi.Lk;  // keys
     // A segment longer than the caller's max_seqlen breaks the contract the host sized the
     // 32-bit buffer offsets by: its rows are left unwritten rather than addressed.
     if (L > p.max_seqlen || Lk > p.max_seqlen_k || Lk < 0) return;

@@ -89,25 +89,25 @@ def test_workspace_size_is_host_arithmetic(lib):
     assert rc == 0
     n_long = min(64, 32438 // 65)
     cap = min(64 * 8, (32438 + n_long * 255) // 256)
-    assert size == 256 + 8 * cap
+    assert size == 256 + 16 * cap
     # windowed head_dim 64: tiles of 128 rows (four waves of 32)
     rc, size = _ws(lib, _args(window_left=64, window_right=64))
-    assert rc == 0 and size == 256 + 8 * min(64 * 16, (32438 + n_long * 127) // 128)
+    assert rc == 0 and size == 256 + 16 * min(64 * 16, (32438 + n_long * 127) // 128)
     # every segment fits the short kernel: no workspace
     rc, size = _ws(lib, _args(max_seqlen=64))
     assert rc == 0 and size == 0
     # GQA 4:1 packs 4 heads per tile; head_dim 256 tiles are four 16-row waves: 16-row tiles
     rc, size = _ws(lib, _args(n_heads_q=8, n_heads_kv=2, head_dim=256, max_seqlen=512, n_seq=256, total_tokens=71104))
     assert rc == 0
-    assert size == 256 + 8 * min(256 * 32, (71104 + 256 * 15) // 16)
+    assert size == 256 + 16 * min(256 * 32, (71104 + 256 * 15) // 16)
     # head_dim 128 keeps 32-row waves: 4 heads of 32 rows
     rc, size = _ws(lib, _args(n_heads_q=8, n_heads_kv=2, head_dim=128, max_seqlen=512, n_seq=256, total_tokens=71104))
     assert rc == 0
-    assert size == 256 + 8 * min(256 * 16, (71104 + 256 * 31) // 32)
+    assert size == 256 + 16 * min(256 * 16, (71104 + 256 * 31) // 32)
     # strips of 4 query tiles: min(N * ceil(ceil(S/256)/4), (tiles_by_tokens + N_long*3) // 4)
     rc, size = _ws(lib, _args(strip=4))
     tiles = (32438 + n_long * 255) // 256
-    assert rc == 0 and size == 256 + 8 * min(64 * 2, (tiles + n_long * 3) // 4)
+    assert rc == 0 and size == 256 + 16 * min(64 * 2, (tiles + n_long * 3) // 4)
 
 
 @pytest.mark.parametrize("field,value,status", [
@@ -134,7 +134,7 @@ def test_key_segment_sizes_are_checked_and_size_the_workspace(lib):
     a.total_tokens_k, a.max_seqlen_k = 5000, 300
     rc, size = _ws(lib, a)
     n = a.n_seq
-    assert rc == 0 and size == 256 + 8 * min(n * 1, (a.total_tokens + n * 127) // 128)
+    assert rc == 0 and size == 256 + 16 * min(n * 1, (a.total_tokens + n * 127) // 128)
     rc, size = _ws(lib, _args(max_seqlen=64))  # same queries, keys shared: no tiled work
     assert rc == 0 and size == 0
 
