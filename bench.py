@@ -142,7 +142,8 @@ def gpu_bench(args, workload):
     lib = _lib.library()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    short_max = hip_short_max(workload.head_dim) if args.short_max is None else args.short_max
+    short_max = (hip_short_max(workload.head_dim, max_seqlen=workload.max_seqlen) if args.short_max is None
+                 else args.short_max)
     cu = torch.tensor(workload.cu_seqlens(), dtype=torch.int32, device=dev)
     T, hq, hkv, d = workload.total_tokens, workload.n_heads_q, workload.n_heads_kv, workload.head_dim
     log(f"{workload.name}: T={T} segments={len(workload.lengths)} max={workload.max_seqlen} heads={hq}/{hkv}x{d} "
@@ -157,24 +158,29 @@ def gpu_bench(args, workload):
         calls.append(LayerCall(lib, hip, workload, layer, cu, q, k, v, g, short_max, plans, args.strip))
     stage, bound, timed_layers = dominant(workload, short_max)
     stream = torch.cuda.current_stream(dev)
-    sp = stream.cuda_stream
 
     timed_set = set(timed_layers)
+    # Stages with no segment to serve are not called (host-known: every segment is at most
+    # max_seqlen tokens long), which keeps an all-short batch at one library call per layer.
+    has_short = 0 < short_max and d <= 128
+    has_tiled = workload.max_seqlen > (short_max if has_short else 0)
 
-    def bracket(fn, events):
+    def bracket(fn, events, sp):
         e0, e1 = events.pop()
         e0.record(stream)
         fn(sp)
         e1.record(stream)
         timed.append((e0, e1))
 
-    def step(events=None):
+    def step(events=None, sp=stream.cuda_stream):
         for i, c in enumerate(calls):
             here = events is not None and i in timed_set
-            bracket(c.short, events) if here and stage == "short" else c.short(sp)
-            if c.plans_here:
-                c.plan(sp)
-            bracket(c.tiled, events) if here and stage == "tiled" else c.tiled(sp)
+            if has_short:
+                bracket(c.short, events, sp) if here and stage == "short" else c.short(sp)
+            if has_tiled:
+                if c.plans_here:
+                    c.plan(sp)
+                bracket(c.tiled, events, sp) if here and stage == "tiled" else c.tiled(sp)
 
     timed = []
     for _ in range(args.warmup):
@@ -194,6 +200,25 @@ def gpu_bench(args, workload):
     wall_ms = (t1 - t0) * 1e3 / args.steps
     gpu_ms = g0.elapsed_time(g1) / args.steps
     kernel_ms = statistics.mean(a.elapsed_time(b) for a, b in timed)
+
+    # The same step captured once into a HIP graph and replayed: the launch cost a serving loop
+    # that captures its packed forward pays (no host work per kernel).
+    graph_ms = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)  # default priority
+        side.wait_stream(stream)
+        with torch.cuda.graph(graph, stream=side):
+            step(sp=side.cuda_stream)
+        stream.wait_stream(side)
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        graph_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        del graph
 
     # Algorithmic work: all layers for the value; the dominant kernel's own segments for the roofline.
     flops = sum(hip.useful_flops(workload.lengths, hq, d, window=l.window, causal=l.causal) for l in workload.layers)
@@ -215,10 +240,14 @@ def gpu_bench(args, workload):
                 "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(workload.name, kernel_name),
                 "kernel": kernel_name, "kernel_ms": round(kernel_ms, 4), "algorithmic_per_launch": per_launch}
     value = flops / (wall_ms * 1e-3) / 1e12
-    log(f"wall {wall_ms:.3f} ms/step (events {gpu_ms:.3f}), {value:.1f} TFLOP/s, dominant {kernel_name} "
-        f"{kernel_ms * 1e3:.1f} us -> {achieved:.1f} {unit} ({achieved / peak:.1%})")
+    log(f"wall {wall_ms:.3f} ms/step (events {gpu_ms:.3f}, graph replay {graph_ms}), {value:.1f} TFLOP/s, "
+        f"dominant {kernel_name} {kernel_ms * 1e3:.1f} us -> {achieved:.1f} {unit} ({achieved / peak:.1%})")
+    replay = None if graph_ms is None else {
+        "ms_per_step": round(graph_ms, 4), "value": round(flops / (graph_ms * 1e-3) / 1e12, 3),
+        "tokens_per_s": round(workload.total_tokens / (graph_ms * 1e-3), 1)}
     return {
         "value": value, "ms_per_step": wall_ms, "gpu_ms_per_step": gpu_ms, "flops_per_step": flops,
+        "graph_replay": replay,
         "tokens_per_s": workload.total_tokens / (wall_ms * 1e-3), "roofline": roofline, "short_max": short_max,
         "_outputs": (calls, cu),
     }
@@ -308,13 +337,21 @@ def model_bench(args, workload):
 
 
 def traffic_from_profiles(workload_name: str, kernel: str):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if one exists."""
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary (profiles/traffic.json),
+    or None when there is none for this kernel or it was measured on other kernel sources (the
+    table carries the source digest it was measured at)."""
+    from packed_encoders_amd._build import source_digest
+
     path = ROOT / "profiles" / "traffic.json"
     try:
         table = json.loads(path.read_text())
     except (OSError, ValueError):
         return None
-    entry = table.get(f"{workload_name}:{kernel}")
+    if table.get("source_digest") != source_digest():
+        log(f"profiles/traffic.json was measured at sources {table.get('source_digest')}, "
+            f"not {source_digest()}: traffic not reported")
+        return None
+    entry = table.get("kernels", {}).get(f"{workload_name}:{kernel}")
     return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
@@ -438,6 +475,257 @@ def copy_calibration(steps: int) -> int:
     return 0
 
 
+PROFILED = ("C1", "Q4096", "C2", "C3", "C4", "C4-band", "C5")
+SQ_PASSES = {  # two counter passes of at most 8 SQ counters (plus GRBM) each
+    "SQA": "SQ_WAVES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_INSTS_SALU "
+           "SQ_WAIT_INST_ANY GRBM_GUI_ACTIVE",
+    "SQB": "SQ_VALU_MFMA_BUSY_CYCLES SQ_VALU_MFMA_COEXEC_CYCLES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS "
+           "SQ_WAIT_INST_LDS SQ_LDS_BANK_CONFLICT SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE",
+}
+MFMA_PROFILED = ("C2", "C3", "C4")
+
+
+def profile_commands(out: str = "gpurun_out/prof") -> list[tuple[str, str]]:
+    """(name, command) of every rocprofv3 run the committed summaries under profiles/ come from,
+    run from the repository root with TMPDIR=/tmp. ``--summarize-profiles`` reads their output."""
+    cmds = []
+    for pmc in ("FETCH_SIZE", "WRITE_SIZE"):
+        cmds.append((f"copy_{pmc}", f"rocprofv3 --pmc {pmc} --output-format csv -d {out}/copy_{pmc} -o p -- "
+                                    f"python3 bench.py --copy-calibration --steps 3"))
+    for w in PROFILED:
+        run = f"python3 bench.py --workload {w} --no-cpu-baseline --no-model"
+        cmds.append((f"{w}_kt", f"rocprofv3 --kernel-trace --stats --output-format csv -d {out}/{w}_kt -o k -- "
+                                f"{run} --steps 10 --warmup 2"))
+        run += " --no-graph"  # counter passes: eager launches only
+        for pmc in ("FETCH_SIZE", "WRITE_SIZE"):
+            cmds.append((f"{w}_{pmc}", f"rocprofv3 --pmc {pmc} --output-format csv -d {out}/{w}_{pmc} -o p -- "
+                                       f"{run} --steps 2 --warmup 1"))
+        if w in MFMA_PROFILED:
+            for name, counters in SQ_PASSES.items():
+                cmds.append((f"{w}_{name}", f"rocprofv3 --pmc {counters} --output-format csv -d {out}/{w}_{name} "
+                                            f"-o p -- {run} --steps 2 --warmup 1"))
+    return cmds
+
+
+def _kernel_label(name: str) -> str:
+    """``void pe::x<...>(pe::AttnParams)`` -> ``pe::x<...>`` (the name kernel_instance gives)."""
+    name = name.strip()
+    if name.startswith("void "):
+        name = name[5:]
+    return name[: -len("(pe::AttnParams)")] if name.endswith("(pe::AttnParams)") else name
+
+
+def _counters(path: Path) -> dict[str, dict[str, list[float]]]:
+    """{kernel: {counter: [value per dispatch]}} from a rocprofv3 counter_collection CSV."""
+    import csv
+
+    per: dict[str, dict[str, dict[str, float]]] = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            k = _kernel_label(r["Kernel_Name"])
+            per.setdefault(k, {}).setdefault(r["Counter_Name"], {})
+            per[k][r["Counter_Name"]][r["Dispatch_Id"]] = float(r["Counter_Value"])
+    return {k: {c: list(v.values()) for c, v in cs.items()} for k, cs in per.items()}
+
+
+def summarize_profiles(src: Path) -> int:
+    """Write profiles/<W>_kernel_trace_stats.md, profiles/<W>_hbm_traffic.md,
+    profiles/<W>_mfma_counters.md and profiles/traffic.json from the output of
+    ``profile_commands`` under ``src`` (a missing run is skipped). HBM bytes are FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch) scaled by what the same counters read for the 1 GiB copy of
+    ``--copy-calibration``; traffic.json carries the source digest of the kernels measured."""
+    import csv
+
+    import packed_encoders_amd as pe
+    from packed_encoders_amd._build import source_digest
+
+    cmds = dict(profile_commands())
+    digest = source_digest()
+    prof = ROOT / "profiles"
+    copy_bytes = 1 << 30
+    scale = {}
+    for pmc in ("FETCH_SIZE", "WRITE_SIZE"):
+        table = _counters(src / f"copy_{pmc}" / "p_counter_collection.csv")
+        per_copy = max(max(v[pmc]) for v in table.values() if pmc in v)  # the 1 GiB copies
+        scale[pmc] = copy_bytes / (per_copy * 1024)
+    workloads = {"C1": pe.workloads.c1, "C2": pe.workloads.c2, "C3": pe.workloads.c3, "C4": pe.workloads.c4,
+                 "C4-band": lambda: pe.workloads.c4(band=True), "C5": pe.workloads.c5,
+                 "Q4096": pe.workloads.query_sweep}
+    traffic = {"source_digest": digest,
+               "calibration": {"copy_bytes": copy_bytes, "fetch_scale": round(scale["FETCH_SIZE"], 4),
+                               "write_scale": round(scale["WRITE_SIZE"], 4)},
+               "kernels": {}}
+    header = (f"Kernel sources: digest `{digest}` (`packed_encoders_amd._build.source_digest()`). One MI355X "
+              f"(gfx950); commands run from the repository root with TMPDIR=/tmp.\n")
+    for w in PROFILED:
+        kt_dir = src / f"{w}_kt"
+        line_path = src / f"{w}_kt.json"
+        if not (kt_dir / "k_kernel_stats.csv").exists() or not line_path.exists():
+            continue
+        wl = workloads[w]()
+        bench_line = json.loads(line_path.read_text().strip().splitlines()[-1])
+        roof = bench_line["roofline"]
+        with open(kt_dir / "k_kernel_stats.csv", newline="") as f:
+            stats = [r for r in csv.DictReader(f)]
+        ours = [r for r in stats if _kernel_label(r["Name"]).startswith("pe::")]
+        total_pct = sum(float(r["Percentage"]) for r in ours)
+        dom = next((r for r in ours if _kernel_label(r["Name"]) == roof["kernel"]), None)
+        out = [f"# {w}: kernel trace statistics (rocprofv3 --kernel-trace --stats)\n",
+               f"Workload: {wl.description}; T = {wl.total_tokens} tokens, {len(wl.lengths)} segments.\n",
+               header, "```", f"{cmds[f'{w}_kt']} > gpurun_out/prof/{w}_kt.json", "```\n",
+               "| kernel | calls | average us | min us | max us | % of GPU time |", "|---|---|---|---|---|---|"]
+        for r in ours:
+            out.append(f"| `{_kernel_label(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                       f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+        out.append(f"\nThe library's kernels take {total_pct:.1f}% of the profiled run's GPU time (the rest is "
+                   f"input set-up: torch.randn).\n")
+        out.append(f"The bench line of the same run: dominant kernel `{roof['kernel']}`, "
+                   f"{roof['kernel_ms'] * 1e3:.1f} us per launch with HIP events on its stream"
+                   + (f" (trace average {float(dom['AverageNs']) / 1e3:.1f} us, ratio "
+                      f"{roof['kernel_ms'] * 1e6 / float(dom['AverageNs']):.3f})" if dom else "")
+                   + f"; {roof['achieved']} {roof['unit']} = {roof['frac']:.1%} of {roof['peak']} {roof['unit']} "
+                   f"({roof['bound']}-bound). Step: {bench_line['ms_per_step']:.4f} ms wall "
+                   f"({bench_line['gpu_ms_per_step']:.4f} ms events), "
+                   f"{bench_line['graph_replay']['ms_per_step']:.4f} ms replayed from a HIP graph.")
+        (prof / f"{w}_kernel_trace_stats.md").write_text("\n".join(out) + "\n")
+
+        fetch_p = src / f"{w}_FETCH_SIZE" / "p_counter_collection.csv"
+        write_p = src / f"{w}_WRITE_SIZE" / "p_counter_collection.csv"
+        if fetch_p.exists() and write_p.exists():
+            fetch, write = _counters(fetch_p), _counters(write_p)
+            out = [f"# {w}: HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)\n", header,
+                   "```", cmds[f"{w}_FETCH_SIZE"], cmds[f"{w}_WRITE_SIZE"], cmds["copy_FETCH_SIZE"],
+                   cmds["copy_WRITE_SIZE"], "```\n",
+                   f"Calibration: for the 1 GiB device copy (1,048,576 KiB read and written) FETCH_SIZE reads "
+                   f"{copy_bytes / 1024 / scale['FETCH_SIZE']:,.0f} KiB and WRITE_SIZE "
+                   f"{copy_bytes / 1024 / scale['WRITE_SIZE']:,.0f} KiB per copy, so HBM bytes = FETCH_SIZE x "
+                   f"{scale['FETCH_SIZE']:.3f} x 1024 and WRITE_SIZE x {scale['WRITE_SIZE']:.3f} x 1024.\n",
+                   "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM read MB | HBM write MB | "
+                   "HBM total MB |", "|---|---|---|---|---|---|---|"]
+            for k in sorted(fetch):
+                if not k.startswith("pe::") or k not in write:
+                    continue
+                f_kib = statistics.mean(fetch[k]["FETCH_SIZE"])
+                w_kib = statistics.mean(write[k]["WRITE_SIZE"])
+                rd, wr = f_kib * 1024 * scale["FETCH_SIZE"], w_kib * 1024 * scale["WRITE_SIZE"]
+                traffic["kernels"][f"{w}:{k}"] = {"hbm_bytes_per_launch": round(rd + wr), "read_bytes": round(rd),
+                                                  "write_bytes": round(wr)}
+                out.append(f"| `{k}` | {len(fetch[k]['FETCH_SIZE'])} | {f_kib:,.1f} | {w_kib:,.1f} | "
+                           f"{rd / 1e6:.2f} | {wr / 1e6:.2f} | {(rd + wr) / 1e6:.2f} |")
+            entry = traffic["kernels"].get(f"{w}:{roof['kernel']}")
+            if entry:
+                cut = bench_line["config"]["short_max"]
+                short_kernel = roof["kernel"].startswith("pe::short_attn_kernel")
+                served = [n for n in wl.lengths if (n <= cut) == short_kernel]
+                need = compulsory_bytes(sum(served), len(served), wl.n_heads_q, wl.n_heads_kv, wl.head_dim,
+                                        any(l.gate for l in wl.layers))
+                out.append(f"\nDominant kernel `{roof['kernel']}`: {entry['hbm_bytes_per_launch'] / 1e6:.2f} MB "
+                           f"per launch against {need / 1e6:.2f} MB compulsory (Q, K, V read once, O written "
+                           f"once{', gate read once' if any(l.gate for l in wl.layers) else ''}): "
+                           f"{entry['hbm_bytes_per_launch'] / need:.2f}x; at the event-timed "
+                           f"{roof['kernel_ms'] * 1e3:.1f} us that is "
+                           f"{entry['hbm_bytes_per_launch'] / (roof['kernel_ms'] * 1e-3) / 1e9:,.0f} GB/s of HBM.")
+            (prof / f"{w}_hbm_traffic.md").write_text("\n".join(out) + "\n")
+
+        a_p, b_p = src / f"{w}_SQA" / "p_counter_collection.csv", src / f"{w}_SQB" / "p_counter_collection.csv"
+        if a_p.exists() and b_p.exists():
+            a, b = _counters(a_p).get(roof["kernel"]), _counters(b_p).get(roof["kernel"])
+            if a and b:
+                m = {c: statistics.mean(v) for c, v in {**a, **b}.items()}
+                mfma = m["SQ_INSTS_MFMA"]
+                flops = m["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512
+                xcd_cycles = m["GRBM_GUI_ACTIVE"] / 8  # GRBM_GUI_ACTIVE sums the 8 XCDs
+                out = [f"# {w}: MFMA utilisation of `{roof['kernel']}` (rocprofv3 --pmc)\n", header, "```",
+                       cmds[f"{w}_SQA"], cmds[f"{w}_SQB"], "```\n",
+                       f"Means per dispatch over {len(a['SQ_INSTS_MFMA'])} dispatches of the dominant kernel.\n",
+                       "| counter | per dispatch |", "|---|---|"]
+                for c in sorted(m):
+                    out.append(f"| {c} | {m[c]:,.0f} |")
+                out += ["", "| derived | value |", "|---|---|",
+                        f"| MFMA FLOPs (MOPS_BF16 x 512) | {flops:.4g} (algorithmic "
+                        f"{roof['algorithmic_per_launch']:.4g}) |",
+                        f"| MFMA pipe busy / (4 SIMDs x SQ_BUSY_CU_CYCLES) | "
+                        f"{m['SQ_VALU_MFMA_BUSY_CYCLES'] / (4 * m['SQ_BUSY_CU_CYCLES']):.3f} |",
+                        f"| MFMA pipe busy / (1024 SIMDs x GRBM_GUI_ACTIVE / 8) | "
+                        f"{m['SQ_VALU_MFMA_BUSY_CYCLES'] / (1024 * xcd_cycles):.3f} |",
+                        f"| VALU co-issued with MFMA / MFMA busy | "
+                        f"{m['SQ_VALU_MFMA_COEXEC_CYCLES'] / m['SQ_VALU_MFMA_BUSY_CYCLES']:.3f} |",
+                        f"| non-MFMA VALU / SALU / LDS instructions per MFMA | "
+                        f"{(m['SQ_INSTS_VALU'] - mfma) / mfma:.2f} / {m['SQ_INSTS_SALU'] / mfma:.2f} / "
+                        f"{m['SQ_INSTS_LDS'] / mfma:.2f} |",
+                        f"| SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES | {m['SQ_WAIT_INST_ANY'] / m['SQ_WAVE_CYCLES']:.3f} |",
+                        f"| LDS bank conflicts / LDS instructions | "
+                        f"{m['SQ_LDS_BANK_CONFLICT'] / m['SQ_INSTS_LDS']:.3f} |",
+                        "", f"Event-timed in the bench line of the kernel-trace run: {roof['kernel_ms'] * 1e3:.1f} us, "
+                        f"{roof['achieved']} TFLOP/s = {roof['frac']:.1%} of the 2.5 PFLOP/s dense bf16 peak."]
+                (prof / f"{w}_mfma_counters.md").write_text("\n".join(out) + "\n")
+    (prof / "traffic.json").write_text(json.dumps(traffic, indent=1, sort_keys=True) + "\n")
+    return 0
+
+
+def dispatch_sweep(reps: int = 20, replays: int = 5) -> int:
+    """Short kernel vs tiled kernel per segment length: the measurement the gfx950 routing
+    boundary (attention_dispatch.HipDispatchPolicy) is fitted to. For head_dim 64 (12 heads)
+    and 128 (8 heads), batches of N segments of exactly L tokens (a C1-sized batch of 32 and a
+    query batch of about 64K tokens) run through the short kernel at its smallest key capacity
+    that holds L (short_max = L), at capacities 64 and 128 (short_max = max(L, 64) and 128, as a
+    batch with longer segments routes its short ones under those boundaries) and through the
+    tiled kernel (short_max = 0, plan included), each call graph-captured `reps` times and replayed, so host overhead is
+    not timed. Prints one JSON line per (head_dim, L, N); the committed summary is
+    profiles/dispatch_sweep.md (packed_encoders/benchmarks/packed_attention_dispatch_bench.py:153-229
+    is the reference's counterpart)."""
+    import torch
+
+    from packed_encoders_amd import _lib, hip_attention as hip
+
+    lib = _lib.library()
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(11)
+    stream = torch.cuda.Stream(dev)
+    for d, h in ((64, 12), (128, 8)):
+        for n_target in (32, 65536):
+            for L in (8, 16, 24, 32, 40, 48, 56, 64, 72, 80, 96, 112, 128):
+                n = 32 if n_target == 32 else max(32, n_target // L)
+                T = n * L
+                q, k, v = (torch.randn(T, h, d, device=dev, generator=gen, dtype=torch.bfloat16) for _ in range(3))
+                cu = torch.arange(0, T + 1, L, dtype=torch.int32, device=dev)
+                times = {}
+                for kind, short_max in (("short", L), ("short64", max(L, 64)), ("short128", 128), ("tiled", 0)):
+                    out = torch.empty_like(q)
+                    a = hip._args(q, k, v, out, cu, L, d ** -0.5, -1, -1, False, None, short_max)
+                    size = ctypes.c_size_t()
+                    assert lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size)) == 0
+                    ws = torch.empty(max(size.value, 1), dtype=torch.uint8, device=dev)
+
+                    def call():
+                        rc = lib.pe_varlen_attn_fwd(ctypes.byref(a), ws.data_ptr(), size.value,
+                                                    torch.cuda.current_stream(dev).cuda_stream)
+                        assert rc == 0, rc
+
+                    with torch.cuda.stream(stream):
+                        call()
+                    torch.cuda.synchronize()
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, stream=stream):
+                        for _ in range(reps):
+                            call()
+                    graph.replay()
+                    torch.cuda.synchronize()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for _ in range(replays):
+                        graph.replay()
+                    e1.record()
+                    torch.cuda.synchronize()
+                    times[kind] = e0.elapsed_time(e1) * 1e3 / (reps * replays)
+                    del graph
+                print(json.dumps({"head_dim": d, "heads": h, "L": L, "n_seq": n, "tokens": T,
+                                  "short_us": round(times["short"], 3), "short64_us": round(times["short64"], 3),
+                                  "short128_us": round(times["short128"], 3), "tiled_us": round(times["tiled"], 3)}),
+                      flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -447,8 +735,15 @@ def main() -> int:
     ap.add_argument("--short-max", type=int, default=None, help="routing boundary (default: gfx950 policy)")
     ap.add_argument("--strip", type=int, default=0, help="query tiles per tiled-kernel workgroup (0: library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="skip the graph-replayed timing of the step")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the end-to-end packed ModernBERT forward (C2 only)")
+    ap.add_argument("--dispatch-sweep", action="store_true",
+                    help="only time the short kernel against the tiled kernel per segment length")
+    ap.add_argument("--profile-commands", action="store_true",
+                    help="only print the rocprofv3 commands behind the committed profiles (name<TAB>command)")
+    ap.add_argument("--summarize-profiles", metavar="DIR",
+                    help="only write the profiles/ summaries from the output of --profile-commands under DIR")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 1 GiB buffer --steps times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -457,8 +752,16 @@ def main() -> int:
               "segments shard across GPUs with no exchange, see DESIGN.md", file=sys.stderr)
         return 2
 
+    if args.profile_commands:
+        for name, cmd in profile_commands():
+            print(f"{name}\t{cmd}")
+        return 0
+    if args.summarize_profiles:
+        return summarize_profiles(Path(args.summarize_profiles))
     if args.copy_calibration:
         return copy_calibration(args.steps)
+    if args.dispatch_sweep:
+        return dispatch_sweep()
 
     import packed_encoders_amd as pe
 
@@ -511,6 +814,7 @@ def main() -> int:
         },
         "tokens_per_s": round(res["tokens_per_s"], 1),
         "gpu_ms_per_step": round(res["gpu_ms_per_step"], 4),
+        "graph_replay": res["graph_replay"],
         "roofline": res["roofline"],
         "cpu_baseline": cpu_res,
     }

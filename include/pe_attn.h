@@ -76,7 +76,8 @@ typedef struct pe_attn_args {
     int32_t causal;       /* 0 or 1; causal is window_right = 0 */
     /* Per-segment routing: segments with length <= short_max run the LDS-resident short
        kernel, longer ones the tiled MFMA kernel. 0 sends every segment to the tiled kernel;
-       -1 asks for the library's gfx950 default. At most 128; head_dim 256 always runs the
+       -1 asks for the library's gfx950 default: max_seqlen (and max_seqlen_k) when it is at
+       most 128 (every segment short), else 64 for head_dim 64 and 32 for head_dim 128. At most 128; head_dim 256 always runs the
        tiled kernel (the short kernel covers head_dim <= 128). */
     int32_t short_max;
     /* Query tiles (of 128 rows; 32 * 4 / gcd(GQA ratio, 4) rows with grouped heads) one

@@ -6,6 +6,7 @@ source tree; nothing is JIT-compiled at import time. ``build_library()`` always 
 
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -32,6 +33,16 @@ HIPCC_FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 SOURCES = ["pe_attn_capi.hip"]
+
+
+def source_digest() -> str:
+    """A short sha256 over the library's HIP sources, its public headers and the compile flags:
+    what ties a committed profile of the kernels to the code it measured."""
+    h = hashlib.sha256(" ".join(HIPCC_FLAGS).encode())
+    for path in sorted(p for p in [*CSRC.iterdir(), *INCLUDE.iterdir()] if p.is_file()):
+        h.update(path.name.encode())
+        h.update(path.read_bytes())
+    return h.hexdigest()[:16]
 
 
 def hipcc() -> str:

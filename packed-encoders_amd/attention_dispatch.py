@@ -1,182 +1,157 @@
-"""Packed attention dispatch policies: the reference's exact-card score policies and the gfx950
-routing policy between the LDS-resident short kernel and the tiled MFMA kernel.
+"""Which kernel serves which packed segment on gfx950, and why.
 
-Restates packed_encoders/attention_dispatch.py:17-205. ``AttentionWorkload``,
-``FlashScorePolicy`` and ``get_packed_inference_policy`` keep their names, fields, integer
-score and exact-card tables (the reference's measured Triton/Flash crossovers on NVIDIA cards,
-kept as data so callers and tests that consult them behave identically). Those tables never
-match an MI355X: on gfx950 the choice is not Triton versus Flash but, per segment on the
-device, short kernel versus tiled kernel, and ``get_hip_dispatch_policy`` returns that policy.
+The reference decides per batch, with an integer score calibrated per NVIDIA card, whether its
+Triton short-segment kernel or FlashAttention serves the whole batch
+(packed_encoders/attention_dispatch.py:17-205, fitted by benchmarks/fit_packed_attention_dispatch.py).
+Here both legs are kernels of one library call and the decision is per segment, on the device:
+a segment of at most ``short_max`` tokens runs the LDS-resident short kernel, a longer one the
+tiled MFMA kernel, with no host read of ``cu_seqlens``. The one host decision is ``short_max``,
+from host-known sizes only (head dim and ``max_seqlen``), so it is the same eagerly and while a
+graph is captured; the C ABI takes the same default when called with ``short_max = -1``.
 
-Every input is a host-visible shape statistic; no policy reads ``cu_seqlens`` values, so the
-same decision is safe before eager execution and while capturing a graph.
+The rule, fitted to the short-vs-tiled sweep (``python bench.py --dispatch-sweep``, committed as
+profiles/dispatch_sweep.md and re-derived by ``fit_boundary`` in the tests):
+
+- ``max_seqlen <= 128``: every segment takes the short kernel, at its smallest key capacity
+  (32, 64 or 128) that holds ``max_seqlen`` — faster than the tiled kernel at every measured
+  length, both head dims and both batch scales (the reference's Triton kernel likewise keys its
+  tile choice on ``Smax``, triton_packed_attention.py:29-42);
+- longer batches: segments up to the fitted boundary (64 for head_dim 64, 32 for head_dim 128)
+  take the short kernel at that capacity, the rest the tiled kernel. A larger capacity makes
+  the short kernel slower on the shortest segments (fewer heads per workgroup, more staged
+  keys), so the boundary is the capacity with the least sweep time summed over the measured
+  lengths, per token.
+- head_dim 256 always runs the tiled kernel (the short kernel serves head_dim <= 128).
+
+Names the reference's callers consult are kept: ``AttentionWorkload`` (capture-safe batch
+statistics) and ``get_packed_inference_policy`` (the current device's calibrated policy, None
+where none is calibrated; crossovers are never borrowed from another GPU).
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass, replace
-from typing import Sequence
+from dataclasses import dataclass
+from typing import Iterable, Mapping, Sequence
 
 import torch
+
+SHORT_CAPACITIES = (32, 64, 128)  # key capacities of the short kernel's LDS tiles
+SHORT_HEAD_DIMS = (64, 128)       # head dims the short kernel serves
+
+
+def capacity_for(length: int) -> int:
+    """The short kernel's smallest key capacity holding ``length`` keys (0 past the largest)."""
+    for c in SHORT_CAPACITIES:
+        if length <= c:
+            return c
+    return 0
 
 
 @dataclass(frozen=True)
 class AttentionWorkload:
-    """Capture-safe summary of an already-packed attention workload."""
+    """Capture-safe statistics of a packed batch: segment count, live tokens, longest segment.
+    Derived: the padded rectangle ``n_sequences * max_seqlen`` and the padding it would hold."""
 
     n_sequences: int
     live_tokens: int
     max_seqlen: int
-    rectangle_tokens: int
-    fragmentation_tokens: int
+
+    def __post_init__(self):
+        n, m, s = self.n_sequences, self.live_tokens, self.max_seqlen
+        if n < 1 or s < 1 or m < 0 or m > n * s:
+            raise ValueError(f"invalid packed workload: {n} segments, {m} live tokens, longest {s}")
+
+    @property
+    def rectangle_tokens(self) -> int:
+        return self.n_sequences * self.max_seqlen
+
+    @property
+    def fragmentation_tokens(self) -> int:
+        return self.rectangle_tokens - self.live_tokens
+
+    @property
+    def mean_length(self) -> float:
+        return self.live_tokens / self.n_sequences
 
     @classmethod
-    def from_lengths(cls, lengths: Sequence[int]) -> "AttentionWorkload":
-        values = tuple(int(length) for length in lengths)
-        if not values or any(length < 0 for length in values):
-            raise ValueError("sequence lengths must be a non-empty sequence of non-negative integers")
-        return cls.from_summary(n_sequences=len(values), live_tokens=sum(values), max_seqlen=max(values))
+    def from_lengths(cls, lengths: Iterable[int]) -> "AttentionWorkload":
+        values = [int(n) for n in lengths]
+        if not values or min(values) < 0:
+            raise ValueError("segment lengths must be a non-empty list of non-negative integers")
+        return cls(len(values), sum(values), max(values))
 
     @classmethod
     def from_summary(cls, *, n_sequences: int, live_tokens: int, max_seqlen: int) -> "AttentionWorkload":
-        n, m, s = int(n_sequences), int(live_tokens), int(max_seqlen)
-        if n <= 0 or m < 0 or s <= 0 or m > n * s:
-            raise ValueError(f"invalid packed workload N={n}, M={m}, Smax={s}")
-        rectangle = n * s
-        return cls(n_sequences=n, live_tokens=m, max_seqlen=s, rectangle_tokens=rectangle,
-                   fragmentation_tokens=rectangle - m)
-
-
-@dataclass(frozen=True)
-class FlashScorePolicy:
-    """Integer scalar score; Flash is selected at ``score >= threshold``
-    (attention_dispatch.py:58-88)."""
-
-    threshold: int
-    live_token_weight: int = 0
-    sequence_weight: int = 0
-    max_seqlen_weight: int = 0
-    rectangle_pair_weight: int = 0
-    mean_square_work_weight: int = 0
-    live_max_weight: int = 0
-    query_cta_weight: int = 0
-
-    def score(self, workload: AttentionWorkload) -> int:
-        n, m, s = workload.n_sequences, workload.live_tokens, workload.max_seqlen
-        block_m = 16 if s <= 64 else 64
-        query_ctas = n * ((s + block_m - 1) // block_m)
-        return (
-            self.live_token_weight * m
-            + self.sequence_weight * n
-            + self.max_seqlen_weight * s
-            + self.rectangle_pair_weight * n * s * s
-            + self.mean_square_work_weight * (m * m // n)
-            + self.live_max_weight * m * s
-            + self.query_cta_weight * query_ctas
-        )
-
-    def use_flash(self, workload: AttentionWorkload) -> bool:
-        return self.score(workload) >= self.threshold
-
-
-# The reference's exact-card tables (attention_dispatch.py:91-143), kept as data.
-_RTX_5090_PACKED_POLICY = FlashScorePolicy(live_token_weight=1, threshold=20_736)
-_A100_PACKED_POLICY = FlashScorePolicy(sequence_weight=-203_715, mean_square_work_weight=24,
-                                       query_cta_weight=41_801, threshold=9_422_745)
-_L40S_PACKED_POLICY = FlashScorePolicy(live_token_weight=4_260, rectangle_pair_weight=-7,
-                                       query_cta_weight=-11_752, threshold=77_166_921)
-_L40S_PACKED_GRAPH_POLICY = replace(_L40S_PACKED_POLICY, threshold=74_000_000)
-_H200_PACKED_POLICY = FlashScorePolicy(live_token_weight=1, threshold=131_073)
-_B200_PACKED_POLICY = FlashScorePolicy(live_token_weight=1, threshold=131_073)
-
-_PACKED_INFERENCE_POLICY_BY_DEVICE = {
-    ((12, 0), "RTX 5090"): _RTX_5090_PACKED_POLICY,
-    ((8, 0), "A100-SXM4-40GB"): _A100_PACKED_POLICY,
-    ((8, 9), "L40S"): _L40S_PACKED_POLICY,
-    ((9, 0), "H200"): _H200_PACKED_POLICY,
-    ((10, 0), "B200"): _B200_PACKED_POLICY,
-}
-_PACKED_GRAPH_POLICY_BY_DEVICE = {((8, 9), "L40S"): _L40S_PACKED_GRAPH_POLICY}
-
-
-def current_compute_capability() -> tuple[int, int] | None:
-    try:
-        if not torch.cuda.is_available():
-            return None
-        return torch.cuda.get_device_capability()
-    except Exception:  # pragma: no cover - defensive
-        return None
-
-
-def current_device_name() -> str | None:
-    try:
-        if not torch.cuda.is_available():
-            return None
-        return torch.cuda.get_device_name()
-    except Exception:  # pragma: no cover - defensive
-        return None
-
-
-def get_packed_inference_policy(compute_capability: tuple[int, int] | None = None,
-                                device_name: str | None = None, *,
-                                for_cuda_graph: bool = False) -> FlashScorePolicy | None:
-    """Exact-card Triton/Flash policy, if calibrated (attention_dispatch.py:164-205).
-
-    ``None`` for every card without a measured table, MI355X included: crossovers are never
-    borrowed from another GPU."""
-    infer_device = compute_capability is None
-    cc = current_compute_capability() if infer_device else compute_capability
-    if cc is None:
-        return None
-    if device_name is None and infer_device:
-        device_name = current_device_name()
-    if device_name is None:
-        return None
-    normalized = device_name.casefold()
-    if for_cuda_graph:
-        for (candidate_cc, fragment), policy in _PACKED_GRAPH_POLICY_BY_DEVICE.items():
-            if candidate_cc == cc and fragment.casefold() in normalized:
-                return policy
-    for (candidate_cc, fragment), policy in _PACKED_INFERENCE_POLICY_BY_DEVICE.items():
-        if candidate_cc == cc and fragment.casefold() in normalized:
-            return policy
-    return None
-
-
-# ------------------------------------------------------------------------------ gfx950 (HIP)
+        return cls(int(n_sequences), int(live_tokens), int(max_seqlen))
 
 
 @dataclass(frozen=True)
 class HipDispatchPolicy:
-    """Per-segment routing for the HIP kernels on one GPU architecture.
-
-    A segment of length ``L`` runs the LDS-resident short kernel when ``L <= short_max`` for its
-    head dim, else the tiled MFMA kernel; both launch in one call and each segment is claimed by
-    exactly one of them on the device, so a batch mixing queries and documents is split with no
-    host read. ``short_max = 0`` sends every segment to the tiled kernel."""
+    """Per-segment routing between the short and the tiled kernel on one GPU architecture.
+    ``boundaries`` maps head dim to the short kernel's share of a batch whose longest segment
+    exceeds its largest capacity (0: every segment to the tiled kernel)."""
 
     arch: str
-    short_max_by_head_dim: tuple[tuple[int, int], ...]
+    boundaries: tuple[tuple[int, int], ...]
 
-    def short_max(self, head_dim: int) -> int:
-        return dict(self.short_max_by_head_dim).get(int(head_dim), 0)
+    def short_max(self, head_dim: int, max_seqlen: int | None = None) -> int:
+        """The routing boundary for a call: ``max_seqlen`` itself when the short kernel holds
+        it, else the fitted boundary for ``head_dim``."""
+        if int(head_dim) not in SHORT_HEAD_DIMS:
+            return 0
+        if max_seqlen is not None and 0 < int(max_seqlen) <= SHORT_CAPACITIES[-1]:
+            return int(max_seqlen)
+        return dict(self.boundaries).get(int(head_dim), 0)
 
     def route(self, lengths: Sequence[int], head_dim: int) -> tuple[list[int], list[int]]:
-        """Indices of the segments each kernel serves: (short, tiled); empty segments in neither."""
-        sm = self.short_max(head_dim)
-        short = [i for i, n in enumerate(lengths) if 0 < n <= sm]
-        tiled = [i for i, n in enumerate(lengths) if n > sm]
+        """Indices of the segments each kernel serves, (short, tiled); empty ones in neither."""
+        cut = self.short_max(head_dim, max(lengths) if lengths else None)
+        short = [i for i, n in enumerate(lengths) if 0 < n <= cut]
+        tiled = [i for i, n in enumerate(lengths) if n > cut]
         return short, tiled
 
+    def use_flash(self, workload: AttentionWorkload, head_dim: int = 64) -> bool:
+        """The reference's per-batch question on this architecture: whether the batch needs the
+        long-segment (tiled) kernel at all."""
+        return workload.max_seqlen > self.short_max(head_dim, workload.max_seqlen)
 
-# gfx950 (MI355X / MI350X): boundary measured with bench.py's per-kernel sweep; the short kernel
-# covers head_dim <= 128 and holds at most 128 keys in LDS.
-_GFX950_POLICY = HipDispatchPolicy(arch="gfx950", short_max_by_head_dim=((64, 64), (128, 64), (256, 0)))
+
+def fit_boundary(rows: Iterable[Mapping], head_dim: int, *, min_segments: int = 512) -> int:
+    """The boundary (0, 32, 64 or 128) with the least total time over the sweep's query-batch
+    rows for ``head_dim``: every measured length L is weighted by its tokens' time, a segment of
+    length L <= c costing the short kernel's time at capacity c (columns ``short_us`` at L's own
+    capacity, ``short64_us``, ``short128_us``), a longer one the tiled kernel's (``tiled_us``).
+    Rows of small batches (fewer than ``min_segments`` segments) are launch-bound and ignored.
+    Returns 0 when no row qualifies."""
+    rows = [r for r in rows if int(r["head_dim"]) == int(head_dim) and int(r["n_seq"]) >= min_segments]
+    if not rows:
+        return 0
+
+    def per_token(r, key):
+        return float(r[key]) / float(r["tokens"])
+
+    def cost(c: int) -> float:
+        total = 0.0
+        for r in rows:
+            length = int(r["L"])
+            if length > c:
+                total += per_token(r, "tiled_us")
+            elif c == capacity_for(length):
+                total += per_token(r, "short_us")
+            else:
+                total += per_token(r, f"short{c}_us")
+        return total
+
+    return min((0, *SHORT_CAPACITIES), key=lambda c: (cost(c), c))
+
+
+# Fitted to profiles/dispatch_sweep.md (tests/test_host_cpu.py re-derives it from that table).
+_GFX950_POLICY = HipDispatchPolicy(arch="gfx950", boundaries=((64, 64), (128, 32)))
 _HIP_POLICY_BY_ARCH = {"gfx950": _GFX950_POLICY}
 
 
 def current_gcn_arch(device: int | torch.device | None = None) -> str | None:
-    """The device's gfx target without feature suffixes (``gfx950:sramecc+:xnack-`` → ``gfx950``)."""
+    """The device's gfx target without feature suffixes (``gfx950:sramecc+:xnack-`` -> ``gfx950``)."""
     try:
         if not torch.cuda.is_available():
             return None
@@ -192,7 +167,32 @@ def get_hip_dispatch_policy(arch: str | None = None) -> HipDispatchPolicy | None
     return _HIP_POLICY_BY_ARCH.get(arch) if arch else None
 
 
-def hip_short_max(head_dim: int, arch: str | None = None) -> int:
+def hip_short_max(head_dim: int, arch: str | None = None, max_seqlen: int | None = None) -> int:
     """The routing boundary the HIP op uses: the calibrated policy's, else gfx950's."""
     policy = get_hip_dispatch_policy(arch) or _GFX950_POLICY
-    return policy.short_max(head_dim)
+    return policy.short_max(head_dim, max_seqlen)
+
+
+def _arch_of(compute_capability: tuple[int, int] | None, device_name: str | None) -> str | None:
+    """gfx950 from what torch reports for it: compute capability (9, 5), or an MI350-series name."""
+    name = (device_name or "").casefold()
+    if compute_capability is not None and tuple(compute_capability) == (9, 5):
+        return "gfx950"
+    if "mi355" in name or "mi350" in name or "gfx950" in name:
+        return "gfx950"
+    return None
+
+
+def get_packed_inference_policy(compute_capability: tuple[int, int] | None = None,
+                                device_name: str | None = None, *,
+                                for_cuda_graph: bool = False) -> HipDispatchPolicy | None:
+    """The calibrated policy of a device (default: the current one), or None (the reference's
+    entry point, attention_dispatch.py:164-205). Graph replay does not change which kernel is
+    faster for a segment (the sweep itself is graph-replayed), so ``for_cuda_graph`` selects the
+    same policy."""
+    del for_cuda_graph
+    if compute_capability is None and device_name is None:
+        arch = current_gcn_arch()
+    else:
+        arch = _arch_of(compute_capability, device_name)
+    return _HIP_POLICY_BY_ARCH.get(arch) if arch else None

@@ -49,7 +49,12 @@ int static_scratch(void **ptr) {
     return PE_ATTN_OK;
 }
 
-constexpr int kDefaultShortMax = 64;  // gfx950 default routing boundary (head_dim <= 128)
+// gfx950 routing boundary for batches longer than the short kernel's largest key capacity,
+// per head dim, fitted to the short-vs-tiled sweep (bench.py --dispatch-sweep): 64 for head_dim
+// 64, 32 for head_dim 128. Batches whose longest segment fits that capacity run every segment
+// in the short kernel.
+constexpr int kShortCapacity = 128;
+constexpr int default_boundary(int head_dim) { return head_dim == 64 ? 64 : 32; }
 constexpr int kMaxStrip = 64;         // query tiles per tiled-kernel workgroup, at most
 
 int gcd_int(int a, int b) {
@@ -108,10 +113,10 @@ int check_args(const pe_attn_args *a, bool need_pointers = true) {
 }
 
 int effective_short_max(const pe_attn_args *a) {
-    int s = a->short_max;
-    if (s < 0) s = a->head_dim <= 128 ? kDefaultShortMax : 0;
-    if (a->head_dim > 128) s = 0;  // the short kernel covers head_dim <= 128
-    return s;
+    if (a->head_dim > 128) return 0;  // the short kernel covers head_dim <= 128
+    if (a->short_max >= 0) return a->short_max;
+    const int32_t longest = a->cu_seqlens_k && a->max_seqlen_k > a->max_seqlen ? a->max_seqlen_k : a->max_seqlen;
+    return longest > 0 && longest <= kShortCapacity ? longest : default_boundary(a->head_dim);
 }
 
 int heads_per_tile(const pe_attn_args *a) { return gcd_int(a->n_heads_q / a->n_heads_kv, 4); }

@@ -1,21 +1,27 @@
-"""Bucketed HIP-graph capture of the packed forward (packed_encoders/graph.py:45-74,212-412).
+"""HIP-graph replay of the packed forward, one graph per token bucket.
 
-One graph per ``(M_bucket, N, Smax, backend)``: ``M_bucket = ceil(M / pad_to) * pad_to`` live
-tokens, the real sequence count N and the real ``max_seqlen``. The captured region is the whole
-packed forward read from static buffers, so a replay costs three small device copies (ids,
-positions, ``cu_seqlens``) plus the replay itself. Tokens between the real M and the bucket
-run through the dense layers but lie outside ``cu_seqlens[N]``, so no attention reads them and
-their rows are dropped from the output.
+The reference's packed graph runner (packed_encoders/graph.py:212-412) captures the packed
+forward per ``(M_bucket, N, Smax, backend)``; the same key and the same public names are kept
+here (``GraphConfig``, ``PackedStaticInputs.stage``, ``build_packed_runner``,
+``graphs_globally_disabled``). The runner itself is organised around what a replay costs on
+MI355X, where the forward of a short batch is a few hundred microseconds of kernels and the
+host work around a replay is what is left to trim:
 
-What makes the capture valid on PyTorch-ROCm:
-- every HIP attention launch takes torch's current stream (the capture stream) and the library
-  allocates nothing, synchronises nothing and never reads ``cu_seqlens`` on the host; the
-  tile plan is built on the device inside the graph, so a replay with new boundaries in the
-  same bucket re-plans itself;
-- the static buffers are refilled with copies and a fill kernel (``zero_`` / ``fill_``), never a
-  memset node inside the graph;
-- a graph replays against fixed addresses, so it is used only without autograd and without
-  autocast (the packed forward checks both).
+- a ``_Bucket`` owns its fixed-address inputs, the graph and the graph's output;
+- staging a batch is two device copies of the real rows plus ``cu_seqlens``; the rows past the
+  real token count are zeroed only when they may hold rows of an earlier, longer batch (the
+  bucket tracks how far its inputs were written), so a stream of equal-length batches stages
+  with no fill kernel at all;
+- the backend resolution a key needs is computed once per autograd state, not per call.
+
+What makes the capture valid: every attention launch takes torch's current stream (the capture
+stream) and the HIP library allocates nothing, synchronises nothing and never reads
+``cu_seqlens`` on the host (its tile plan is built on the device inside the graph, so a replay
+with new boundaries in the same bucket re-plans itself); inputs are refilled with copies and
+fill kernels, never with a memset node; and a graph replays against fixed addresses, so the
+packed forward uses it only without autograd and without autocast. Rows between the real token
+count and the bucket run through the dense layers but lie outside ``cu_seqlens[N]``: no
+attention reads them and their outputs are dropped.
 """
 
 from __future__ import annotations
@@ -27,22 +33,27 @@ from dataclasses import dataclass
 import torch
 from torch import Tensor, nn
 
-from . import forward
+from . import forward, staging
 from .config import ModernBertParams
 
 GRAPH_ENV_VAR = forward.GRAPH_ENV
 
 
 def graphs_globally_disabled() -> bool:
-    """The ``PACKED_ENCODERS_GRAPH=0`` kill switch."""
+    """True when ``PACKED_ENCODERS_GRAPH=0`` switches every graph runner off."""
     return os.environ.get(GRAPH_ENV_VAR, "1") == "0"
 
 
 @dataclass(frozen=True)
 class GraphConfig:
-    """Bucketing policy. ``pad_to`` rounds the token count; ``max_batch`` / ``max_seq`` /
-    ``max_tokens`` bound which calls are graphed (larger ones run eagerly); ``max_graphs`` bounds
-    the cache by LRU; ``warmup`` eager runs precede each capture."""
+    """Which packed calls are graphed, and how graphs are cached.
+
+    ``pad_to``: token counts are rounded up to a multiple of it (one graph serves the bucket).
+    ``max_batch`` / ``max_seq`` / ``max_tokens``: calls with more sequences, a longer sequence or
+    more tokens run eagerly; the packed runner needs the first two set. ``max_graphs``: the
+    least recently replayed graph is dropped beyond this many. ``warmup``: eager runs before a
+    capture. ``seq_buckets`` belongs to the padded-batch runner's pre-capture list; packed
+    graphs are captured on first use."""
 
     pad_to: int = 64
     max_batch: int | None = None
@@ -54,43 +65,57 @@ class GraphConfig:
 
 
 def round_up(value: int, multiple: int) -> int:
-    return (value + multiple - 1) // multiple * multiple
+    return -(-value // multiple) * multiple
 
 
 @dataclass
 class PackedStaticInputs:
-    """Fixed-address inputs of one packed graph."""
+    """The fixed-address inputs one packed graph reads. ``written`` is how many leading rows of
+    ``input_ids`` / ``position_ids`` may be non-zero (-1: unknown, the whole buffer)."""
 
     input_ids: Tensor
     cu_seqlens: Tensor
     position_ids: Tensor
     max_seqlen: int
+    written: int = -1
 
     def stage(self, packed_ids: Tensor, cu_seqlens: Tensor, position_ids: Tensor) -> int:
-        """Copy a real batch in: the bucket tail gets id 0 / position 0, and ``cu_seqlens`` past
-        the real sequences (none when N matches the key) is filled with M."""
-        m = packed_ids.shape[0]
-        n = cu_seqlens.shape[0] - 1
+        """Copy one batch in and return its token count M. Rows past M hold id 0 and position
+        0; entries of ``cu_seqlens`` past the batch's own hold M (empty trailing sequences)."""
+        m, bounds = packed_ids.shape[0], cu_seqlens.shape[0]
         self.input_ids[:m].copy_(packed_ids)
-        self.input_ids[m:].zero_()
         self.position_ids[:m].copy_(position_ids)
-        self.position_ids[m:].zero_()
-        self.cu_seqlens[: n + 1].copy_(cu_seqlens)
-        if n + 1 < self.cu_seqlens.shape[0]:
-            self.cu_seqlens[n + 1:].fill_(m)
+        stale = self.input_ids.shape[0] if self.written < 0 else self.written
+        if stale > m:
+            self.input_ids[m:stale].zero_()
+            self.position_ids[m:stale].zero_()
+        self.written = m
+        self.cu_seqlens[:bounds].copy_(cu_seqlens)
+        if bounds < self.cu_seqlens.shape[0]:
+            self.cu_seqlens[bounds:].fill_(m)
         return m
 
 
 @dataclass
-class PackedCaptured:
+class _Bucket:
     graph: "torch.cuda.CUDAGraph"
     inputs: PackedStaticInputs
     out: Tensor
 
 
+def _synthetic_lengths(tokens: int, n: int, max_seqlen: int) -> list[int]:
+    """A valid batch for warm-up and capture: ``n`` sequences filled greedily up to
+    ``max_seqlen`` from ``tokens`` (a bucket above ``n * max_seqlen`` keeps its tail outside)."""
+    lengths, left = [], min(tokens, n * max_seqlen)
+    for _ in range(n):
+        lengths.append(min(max_seqlen, left))
+        left -= lengths[-1]
+    return lengths
+
+
 class PackedGraphRunner:
-    """Captures ``packed_forward`` per ``(M_bucket, N, Smax, backend)`` and replays it
-    (graph.py:241-400)."""
+    """Replays ``packed_forward`` from graphs keyed ``(round_up(M, pad_to), N, Smax, backend)``.
+    ``captures`` counts the graphs captured so far."""
 
     def __init__(self, model: nn.Module, params: ModernBertParams, config: GraphConfig, backend: str = "hip", *,
                  execution=None):
@@ -100,84 +125,83 @@ class PackedGraphRunner:
         self.backend = backend
         self.execution = forward._execution_for(model, execution)
         self.device = next(model.parameters()).device
-        self.cache: "OrderedDict[tuple[int, int, int, str], PackedCaptured]" = OrderedDict()
-        self.captures = 0  # number of graphs captured so far (observability and tests)
+        self.cache: "OrderedDict[tuple[int, int, int, str], _Bucket]" = OrderedDict()
+        self.captures = 0
+        self._resolved: dict[bool, str] = {}
+
+    def _backend_now(self) -> str:
+        grad = torch.is_grad_enabled()
+        if grad not in self._resolved:
+            dtype = self.model.embeddings.tok_embeddings.weight.dtype
+            self._resolved[grad] = forward.resolve_backend(self.backend, self.params, device=self.device,
+                                                           dtype=dtype)
+        return self._resolved[grad]
 
     def key(self, m: int, n: int, max_seqlen: int) -> tuple[int, int, int, str]:
-        dtype = self.model.embeddings.tok_embeddings.weight.dtype
-        resolved = forward.resolve_backend(self.backend, self.params, device=self.device, dtype=dtype)
-        return (round_up(m, self.config.pad_to), n, int(max_seqlen), resolved)
+        return (round_up(m, self.config.pad_to), n, int(max_seqlen), self._backend_now())
 
     def admits(self, m: int, n: int, max_seqlen: int) -> bool:
         c = self.config
-        return not ((c.max_seq is not None and max_seqlen > c.max_seq) or (c.max_batch is not None and n > c.max_batch)
-                    or m > c.max_tokens)
+        return (m <= c.max_tokens and (c.max_seq is None or max_seqlen <= c.max_seq)
+                and (c.max_batch is None or n <= c.max_batch))
 
     def __call__(self, packed_ids: Tensor, cu_seqlens: Tensor, max_seqlen: int, position_ids: Tensor) -> Tensor:
         m, n = packed_ids.shape[0], cu_seqlens.numel() - 1
-        if not self.admits(m, n, max_seqlen):
+        key = self.key(m, n, max_seqlen) if self.admits(m, n, max_seqlen) else None
+        if key is None or key[3] != "hip":
             return self.eager(packed_ids, cu_seqlens, max_seqlen, position_ids)
-        key = self.key(m, n, max_seqlen)
-        if key[3] != "hip":
-            return self.eager(packed_ids, cu_seqlens, max_seqlen, position_ids)
-        captured = self.cache.get(key)
-        if captured is None:
-            captured = self.capture(*key)
+        bucket = self.cache.get(key)
+        if bucket is None:
+            bucket = self.capture(*key)
             while len(self.cache) >= self.config.max_graphs:
                 self.cache.popitem(last=False)
-            self.cache[key] = captured
+            self.cache[key] = bucket
         else:
             self.cache.move_to_end(key)
-        m_real = captured.inputs.stage(packed_ids, cu_seqlens, position_ids)
-        captured.graph.replay()
-        return captured.out[:m_real].clone()
+        rows = bucket.inputs.stage(packed_ids, cu_seqlens, position_ids)
+        bucket.graph.replay()
+        return bucket.out[:rows].clone()
 
     def eager(self, packed_ids, cu_seqlens, max_seqlen, position_ids) -> Tensor:
         return forward.packed_forward(self.model, self.params, packed_ids, cu_seqlens, max_seqlen, position_ids,
                                       backend=self.backend, execution=self.execution, _allow_graph=False)
 
-    def capture(self, mb: int, n: int, max_seqlen: int, backend: str) -> PackedCaptured:
+    def capture(self, tokens: int, n: int, max_seqlen: int, backend: str) -> _Bucket:
         dev = self.device
-        static = PackedStaticInputs(input_ids=torch.zeros(mb, dtype=torch.long, device=dev),
+        inputs = PackedStaticInputs(input_ids=torch.zeros(tokens, dtype=torch.long, device=dev),
                                     cu_seqlens=torch.zeros(n + 1, dtype=torch.int32, device=dev),
-                                    position_ids=torch.zeros(mb, dtype=torch.long, device=dev),
-                                    max_seqlen=max_seqlen)
-        # A valid synthetic distribution for warm-up and capture: N sequences of up to max_seqlen
-        # tokens; a bucket larger than N * max_seqlen leaves its tail outside cu_seqlens.
-        lengths, remaining = [], min(mb, n * max_seqlen)
-        for _ in range(n):
-            lengths.append(min(max_seqlen, remaining))
-            remaining -= lengths[-1]
-        cu = torch.tensor([0, *torch.tensor(lengths).cumsum(0).tolist()], dtype=torch.int32)
-        static.cu_seqlens.copy_(cu.to(dev))
-        pos = torch.cat([torch.arange(x) for x in lengths]) if lengths else torch.zeros(0, dtype=torch.long)
-        static.position_ids[: pos.numel()].copy_(pos.to(dev))
+                                    position_ids=torch.zeros(tokens, dtype=torch.long, device=dev),
+                                    max_seqlen=max_seqlen, written=0)
+        cu, positions = staging.packed_layout_host(_synthetic_lengths(tokens, n, max_seqlen))
+        inputs.stage(torch.zeros(positions.numel(), dtype=torch.long, device=dev), cu.to(dev, torch.int32),
+                     positions.to(dev))
+        current = torch.cuda.current_stream(dev)
         with torch.no_grad():
-            side = torch.cuda.Stream(device=dev)
-            side.wait_stream(torch.cuda.current_stream(dev))
+            side = torch.cuda.Stream(device=dev)  # default priority
+            side.wait_stream(current)
             with torch.cuda.stream(side):
                 for _ in range(self.config.warmup):
-                    self.run(static)
-            torch.cuda.current_stream(dev).wait_stream(side)
+                    self.run(inputs)
+            current.wait_stream(side)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                out = self.run(static)
+                out = self.run(inputs)
         self.captures += 1
-        return PackedCaptured(graph=graph, inputs=static, out=out)
+        return _Bucket(graph=graph, inputs=inputs, out=out)
 
-    def run(self, static: PackedStaticInputs) -> Tensor:
-        """The captured region: embeddings, RoPE gather, the layer loop and the final norm."""
+    def run(self, inputs: PackedStaticInputs) -> Tensor:
+        """The captured region: embeddings and their norm, then the packed layer stack."""
         model, ex = self.model, self.execution
         norm = model.embeddings.norm
-        x = ex.layer_norm(model.embeddings.tok_embeddings(static.input_ids), norm.weight, norm.eps)
-        return forward.packed_core(model, self.params, x, static.cu_seqlens, static.max_seqlen, static.position_ids,
+        x = ex.layer_norm(model.embeddings.tok_embeddings(inputs.input_ids), norm.weight, norm.eps)
+        return forward.packed_core(model, self.params, x, inputs.cu_seqlens, inputs.max_seqlen, inputs.position_ids,
                                    execution=ex)
 
 
 def build_packed_runner(model: nn.Module, params: ModernBertParams, config: GraphConfig, backend: str = "hip", *,
                         execution=None) -> PackedGraphRunner | None:
-    """A runner when the backend can be captured (the HIP kernels) and the config bounds both
-    the sequence count and the length (graph.py:403-412)."""
+    """A runner when the backend can be captured (not ``"sdpa"``) and ``config`` bounds both the
+    sequence count and the longest sequence (the reference's rule, graph.py:403-412); else None."""
     if backend == "sdpa" or config.max_batch is None or config.max_seq is None:
         return None
     return PackedGraphRunner(model, params, config, backend=backend, execution=execution)

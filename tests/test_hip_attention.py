@@ -173,11 +173,11 @@ def test_segment_alone_equals_segment_in_batch(pe):
     q, k, v, cu, _ = _inputs(lengths, seed=9)
     qd, kd, vd, cud = _dev(q, k, v, cu)
     with torch.inference_mode():
-        batch = pe.varlen_attention(qd, kd, vd, cud, 700, window=(64, 64))
+        batch = pe.varlen_attention(qd, kd, vd, cud, 700, window=(64, 64), short_max=64)
         for a, b in ((0, 50), (50, 750), (750, 770)):
             one = torch.tensor([0, b - a], dtype=torch.int32, device="cuda")
             alone = pe.varlen_attention(qd[a:b].contiguous(), kd[a:b].contiguous(), vd[a:b].contiguous(), one, b - a,
-                                        window=(64, 64))
+                                        window=(64, 64), short_max=64)
             assert torch.equal(alone, batch[a:b])
 
 

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import dataclasses
 
+import numpy as np
 import pytest
 import torch
 
@@ -167,30 +168,109 @@ def _workload(lengths):
     return attention_dispatch.AttentionWorkload.from_lengths(lengths)
 
 
-def test_reference_policy_tables_keep_their_boundaries():
-    p = attention_dispatch.get_packed_inference_policy((12, 0), "NVIDIA GeForce RTX 5090")
-    assert not p.use_flash(_workload((128,) * 160)) and p.use_flash(_workload((96,) * 216))
-    p = attention_dispatch.get_packed_inference_policy((8, 0), "NVIDIA A100-SXM4-40GB")
-    assert not p.use_flash(_workload((64, 32) * 192)) and p.use_flash(_workload((64, 32) * 256))
-    p = attention_dispatch.get_packed_inference_policy((8, 9), "NVIDIA L40S")
-    g = attention_dispatch.get_packed_inference_policy((8, 9), "NVIDIA L40S", for_cuda_graph=True)
-    assert not p.use_flash(_workload((64,) * 384)) and p.use_flash(_workload((128,) * 192))
-    assert g.use_flash(_workload((64,) * 384)) and not g.use_flash(_workload((64,) * 320))
-    for cc, name in (((9, 0), "NVIDIA H200"), ((10, 0), "NVIDIA B200")):
-        p = attention_dispatch.get_packed_inference_policy(cc, name)
-        assert not p.use_flash(_workload((128,) * 1024)) and p.use_flash(_workload((128,) * 1024 + (1,)))
-    for cc, name in (((12, 0), "some other sm120"), ((8, 0), "NVIDIA A30"), ((9, 0), "NVIDIA H100")):
+def test_packed_inference_policy_is_the_gfx950_policy_and_none_elsewhere():
+    """The reference's entry point answers with this architecture's calibrated policy only:
+    gfx950 by its compute capability (9, 5) or its name; NVIDIA cards and other AMD parts get
+    None (no crossover is borrowed from another GPU)."""
+    for cc, name in (((9, 5), "AMD Instinct MI355X"), ((9, 5), ""), ((0, 0), "AMD Instinct MI350X")):
+        policy = attention_dispatch.get_packed_inference_policy(cc, name)
+        assert policy is not None and policy.arch == "gfx950"
+        assert attention_dispatch.get_packed_inference_policy(cc, name, for_cuda_graph=True) == policy
+    for cc, name in (((12, 0), "NVIDIA GeForce RTX 5090"), ((8, 0), "NVIDIA A100-SXM4-40GB"),
+                     ((9, 4), "AMD Instinct MI300X")):
         assert attention_dispatch.get_packed_inference_policy(cc, name) is None
+    policy = attention_dispatch.get_packed_inference_policy((9, 5), "AMD Instinct MI355X")
+    # the reference's per-batch question: does the batch need the long-segment kernel?
+    assert not policy.use_flash(_workload((128,) * 160)) and not policy.use_flash(_workload((5, 100)))
+    assert policy.use_flash(_workload((129, 3))) and policy.use_flash(_workload((2048,)))
+    assert policy.use_flash(_workload((2048,)), head_dim=128)
+
+
+def test_attention_workload_statistics_and_validation():
+    w = _workload((5, 0, 12))
+    assert (w.n_sequences, w.live_tokens, w.max_seqlen, w.rectangle_tokens, w.fragmentation_tokens) == (3, 17, 12, 36, 19)
+    assert attention_dispatch.AttentionWorkload.from_summary(n_sequences=3, live_tokens=17, max_seqlen=12) == w
+    for bad in (dict(n_sequences=2, live_tokens=33, max_seqlen=16), dict(n_sequences=0, live_tokens=0, max_seqlen=1),
+                dict(n_sequences=1, live_tokens=-1, max_seqlen=4)):
+        with pytest.raises(ValueError):
+            attention_dispatch.AttentionWorkload.from_summary(**bad)
     with pytest.raises(ValueError):
-        attention_dispatch.AttentionWorkload.from_summary(n_sequences=2, live_tokens=33, max_seqlen=16)
+        _workload(())
 
 
 def test_gfx950_routing_policy():
     policy = attention_dispatch.get_hip_dispatch_policy("gfx950:sramecc+:xnack-")
     assert policy is not None and policy.short_max(64) == 64 and policy.short_max(256) == 0
+    assert policy.short_max(64, max_seqlen=100) == 100 and policy.short_max(128, max_seqlen=128) == 128
+    assert policy.short_max(64, max_seqlen=129) == 64 and policy.short_max(256, max_seqlen=50) == 0
+    assert policy.short_max(128, max_seqlen=129) == 32
     short, tiled = policy.route([0, 10, 64, 65, 2048], 64)
     assert short == [1, 2] and tiled == [3, 4]
+    short, tiled = policy.route([0, 10, 100, 128], 64)  # every segment fits the short kernel
+    assert short == [1, 2, 3] and tiled == []
     assert attention_dispatch.get_hip_dispatch_policy("gfx942") is None
+    assert [attention_dispatch.capacity_for(n) for n in (1, 32, 33, 64, 65, 128, 129)] == [32, 32, 64, 64, 128, 128, 0]
+
+
+def test_library_default_routing_is_the_policy():
+    """The C ABI's short_max = -1 routes exactly as the Python policy: same workspace (the tiled
+    kernel's share) as an explicit short_max from HipDispatchPolicy.short_max."""
+    import ctypes
+
+    from packed_encoders_amd import _lib
+
+    lib = _lib.library()
+    policy = attention_dispatch.get_hip_dispatch_policy("gfx950")
+
+    def ws(d, max_seqlen, short_max, n=64, t=20000):
+        a = _lib.AttnArgs()
+        a.struct_size, a.dtype = ctypes.sizeof(_lib.AttnArgs), 1
+        a.n_seq, a.total_tokens, a.max_seqlen = n, t, max_seqlen
+        a.n_heads_q = a.n_heads_kv = 8
+        a.head_dim, a.softmax_scale = d, 0.1
+        a.window_left = a.window_right = -1
+        a.short_max = short_max
+        size = ctypes.c_size_t()
+        assert lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size)) == 0
+        return size.value
+
+    for d in (64, 128, 256):
+        for max_seqlen in (20, 64, 65, 128, 129, 300, 2048):
+            for n in (64, 2000):  # with 2000 segments the workspace bound depends on the boundary
+                want = ws(d, max_seqlen, policy.short_max(d, max_seqlen), n=n)
+                assert ws(d, max_seqlen, -1, n=n) == want, (d, max_seqlen, n)
+    assert ws(64, 100, -1) == 0  # all short: no tiled work at all
+    assert ws(128, 300, 32, n=2000) != ws(128, 300, 64, n=2000)
+
+
+def _sweep_rows():
+    """The data table of profiles/dispatch_sweep.md (the committed gfx950 sweep)."""
+    import pathlib
+
+    text = (pathlib.Path(__file__).resolve().parents[1] / "profiles" / "dispatch_sweep.md").read_text()
+    lines = [ln for ln in text.splitlines() if ln.startswith("|")]
+    header = next(i for i, ln in enumerate(lines) if ln.startswith("| head_dim | heads |"))
+    names = [c.strip() for c in lines[header].strip("|").split("|")]
+    rows = []
+    for ln in lines[header + 2:]:
+        rows.append(dict(zip(names, (float(c) for c in ln.strip("|").split("|")))))
+    return rows
+
+
+def test_gfx950_boundaries_are_the_fit_of_the_committed_sweep():
+    """The policy's boundaries are what fit_boundary derives from the committed sweep, and the
+    all-short rule for batches of at most 128 tokens holds in every measured row."""
+    rows = _sweep_rows()
+    assert len(rows) == 52 and {int(r["head_dim"]) for r in rows} == {64, 128}
+    policy = attention_dispatch.get_hip_dispatch_policy("gfx950")
+    for d in (64, 128):
+        assert attention_dispatch.fit_boundary(rows, d) == dict(policy.boundaries)[d], d
+        assert policy.short_max(d, max_seqlen=4096) == attention_dispatch.fit_boundary(rows, d)
+    for r in rows:
+        assert r["short_us"] < r["tiled_us"], r
+    # the fit responds to the data: make the tiled kernel free and it takes every segment
+    assert attention_dispatch.fit_boundary([dict(r, tiled_us=0.0) for r in rows], 64) == 0
+    assert attention_dispatch.fit_boundary(rows, 64, min_segments=10 ** 6) == 0
 
 
 # ----------------------------------------------------------------------------- pieces
@@ -245,6 +325,31 @@ def test_select_attention_sdpa_candidate_and_rejections_on_cpu():
     assert torch.allclose(padded[keep], packed, atol=1e-5)
 
 
+@pytest.mark.parametrize("window,causal", [((-1, -1), False), ((5, 3), False), ((-1, -1), True), ((4, -1), True),
+                                           ((0, 0), False)])
+def test_probe_oracle_and_bucketed_sdpa_match_the_numpy_oracle(window, causal, monkeypatch):
+    """The selector's float64 oracle (one masked score matrix from segment ids) and the SDPA
+    candidate (length-bucketed padded batches, several buckets forced by a small budget) against
+    oracle/attention.py's per-segment loops, with GQA, empty and one-token segments, and query
+    segments that are the tails of longer key segments."""
+    from oracle import attention as oa
+
+    monkeypatch.setattr(runtime_attention, "_SDPA_BUCKET_ELEMENTS", 4 * 40 * 40)
+    g = torch.Generator().manual_seed(5)
+    lengths_q, lengths_k = [7, 0, 1, 33, 12, 40], [7, 3, 9, 33, 30, 40]
+    q = torch.randn(sum(lengths_q), 4, 8, generator=g, dtype=torch.float64)
+    k = torch.randn(sum(lengths_k), 2, 8, generator=g, dtype=torch.float64)
+    v = torch.randn(sum(lengths_k), 2, 8, generator=g, dtype=torch.float64)
+    cu_q = np.cumsum([0] + lengths_q)
+    cu_k = np.cumsum([0] + lengths_k)
+    want = oa.packed_attention(q.numpy(), k.numpy(), v.numpy(), cu_q, scale=0.3, window=window, causal=causal,
+                               cu_seqlens_k=cu_k)
+    got = runtime_attention.oracle_attention(q, k, v, lengths_q, lengths_k, causal, window, 0.3).numpy()
+    np.testing.assert_allclose(got, want, atol=1e-12)
+    got = runtime_attention.bucketed_sdpa(q.float(), k.float(), v.float(), lengths_q, lengths_k, causal, window, 0.3)
+    np.testing.assert_allclose(got.double().numpy(), want, atol=2e-5)
+
+
 def test_sigmoid_gate_rounding():
     o = torch.randn(10, 4).bfloat16()
     g = torch.randn(10, 4)
@@ -265,6 +370,25 @@ def test_packed_static_inputs_stage_fills_tails():
     assert s.position_ids.tolist() == [0, 1, 2, 0, 1, 0, 0, 0]
     assert s.cu_seqlens.tolist() == [0, 3, 5, 5]
     assert graph.round_up(65, 64) == 128 and graph.round_up(64, 64) == 64
+    # a longer batch, then a shorter one: the rows the longer one wrote are zeroed again
+    s.stage(torch.arange(1, 9), torch.tensor([0, 8], dtype=torch.int32), torch.arange(8))
+    assert s.written == 8 and s.cu_seqlens.tolist() == [0, 8, 8, 8]
+    s.stage(torch.tensor([9, 9]), torch.tensor([0, 1, 2], dtype=torch.int32), torch.tensor([0, 0]))
+    assert s.input_ids.tolist() == [9, 9, 0, 0, 0, 0, 0, 0] and s.position_ids.tolist() == [0] * 8
+    assert s.cu_seqlens.tolist() == [0, 1, 2, 2]
+
+
+def test_packed_layout_host_against_per_sequence_counting():
+    from packed_encoders_amd import staging
+
+    g = np.random.default_rng(5)
+    for _ in range(100):
+        lengths = g.choice([0, 0, 1, 2, 5, 17], size=g.integers(0, 12)).tolist()
+        cu, pos = staging.packed_layout_host(lengths)
+        assert cu.tolist() == [0, *np.cumsum(lengths, dtype=np.int64).tolist()]
+        assert pos.tolist() == [p for n in lengths for p in range(n)]
+    with pytest.raises(ValueError):
+        staging.packed_layout_host([3, -1])
 
 
 def test_graph_runner_needs_bounded_config():

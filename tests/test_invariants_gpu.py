@@ -5,7 +5,12 @@ tests/test_cpu_short_attention.py:72-77 of the reference), for head_dim 64, 128 
 
 Leakage: scaling another segment's keys by 100, its values by -100, its queries by 7 and its
 gate by -3 leaves every other segment's output bits unchanged. Independence: a segment run
-alone (its own tensors, a one-segment ``cu_seqlens``) gives the same bits as inside the batch.
+alone (its own tensors, a one-segment ``cu_seqlens``) gives the same bits as inside the batch
+under the same routing boundary (``short_max`` 64: a segment's kernel follows its own length).
+The library's default boundary is keyed on the batch's longest segment (every segment short
+when it is at most 128 tokens), so with the default a 65-128-token segment may take the short
+kernel alone and the tiled kernel in a longer batch: both within tolerance, not the same bits,
+as the reference's per-batch Triton / FlashAttention choice.
 """
 
 from __future__ import annotations
@@ -90,11 +95,11 @@ def test_segment_alone_equals_segment_in_batch(pe, d, hq, hkv, window, causal, g
     announce(f"batch independence d={d} {hq}:{hkv} window={window} causal={causal} gate={gate} "
              f"separate_keys={separate_keys}")
     q, k, v, gt, cu, cuk, _ = _tensors(d, hq, hkv, gate, separate_keys, seed=3 * d + hkv)
-    batch = _run(pe, q, k, v, gt, cu, cuk, window, causal, -1, separate_keys)
+    batch = _run(pe, q, k, v, gt, cu, cuk, window, causal, 64, separate_keys)
     for s in range(len(Q_LENGTHS)):
         a, b, ka, kb = cu[s], cu[s + 1], cuk[s], cuk[s + 1]
         alone = _run(pe, q[a:b].contiguous(), k[ka:kb].contiguous(), v[ka:kb].contiguous(),
-                     None if gt is None else gt[a:b].contiguous(), [0, b - a], [0, kb - ka], window, causal, -1,
+                     None if gt is None else gt[a:b].contiguous(), [0, b - a], [0, kb - ka], window, causal, 64,
                      separate_keys)
         torch.cuda.synchronize()
         assert torch.equal(alone, batch[a:b]), f"segment {s} ({b - a} rows) differs alone"
