@@ -112,24 +112,33 @@ def dominant(workload, short_max):
     return "tiled", "hbm", list(range(len(workload.layers)))
 
 
-def kernel_instance(stage, workload, layer, short_max):
-    """The kernel's name as rocprofv3 lists it (template arguments included)."""
-    d = workload.head_dim
-    if stage == "short":
-        sk = 32 if short_max <= 32 else (64 if short_max <= 64 else 128)
-        hpw = (2 if sk == 128 else 4) if d == 64 else (4 if sk == 32 else (2 if sk == 64 else 1))
-        return f"pe::short_attn_kernel<{d}, {sk}, {hpw}, {str(layer.gate).lower()}>"
+def kernel_instance(lib, call, workload):
+    """The name rocprofv3 lists (template arguments included) for the kernels of one layer's
+    call, as the library reports its choice (pe_attn_kernels): (short kernel, long kernel)."""
+    from packed_encoders_amd import _lib
+
+    out = (ctypes.c_int32 * 4)()
+    rc = lib.pe_attn_kernels(ctypes.byref(call.args), out)
+    if rc:
+        raise RuntimeError(f"pe_attn_kernels: {rc}")
+    layer, d = call.layer, workload.head_dim
+    gate = str(layer.gate).lower()
+    win = str(layer.window != (-1, -1) or layer.causal).lower()
     g = math.gcd(workload.n_heads_q // workload.n_heads_kv, 4)
-    bn = 32 if d >= 256 else 64
-    ns = 3 if d == 64 else 2
-    win = layer.window != (-1, -1) or layer.causal
-    flags = f"{str(layer.gate).lower()}, {str(win).lower()}"
-    if d == 256:
-        return f"pe::wide16_attn_kernel<{d}, 4, {g}, {ns}, {flags}>"  # four waves per workgroup
-    if d == 64 and not win:
-        return f"pe::global64_attn_kernel<{g}, {str(layer.gate).lower()}>"
-    name = "tiled_attn_kernel" if d == 64 else "wide_attn_kernel"
-    return f"pe::{name}<{d}, {g}, {bn}, {ns}, {flags}>"
+    short = None
+    if out[0]:
+        sk = out[0]
+        hpw = (2 if sk == 128 else 4) if d == 64 else (4 if sk == 32 else (2 if sk == 64 else 1))
+        short = f"pe::short_attn_kernel<{d}, {sk}, {hpw}, {gate}>"
+    long = {
+        _lib.KERNEL_NONE: None,
+        _lib.KERNEL_TILED: f"pe::tiled_attn_kernel<64, {g}, 64, 3, {gate}, {win}>",
+        _lib.KERNEL_GLOBAL64: f"pe::global64_attn_kernel<{g}, {gate}>",
+        _lib.KERNEL_BAND64: f"pe::band64_attn_kernel<{gate}>",
+        _lib.KERNEL_WIDE: f"pe::wide_attn_kernel<128, {g}, 64, 2, {gate}, {win}>",
+        _lib.KERNEL_WIDE16: f"pe::wide16_attn_kernel<256, 4, {g}, 2, {gate}, {win}>",
+    }[out[1]]
+    return short, long
 
 
 def gpu_bench(args, workload):
@@ -235,7 +244,8 @@ def gpu_bench(args, workload):
         per_launch = compulsory_bytes(sum(served), len(served), hq, hkv, d, layer0.gate)
         achieved = per_launch / (kernel_ms * 1e-3) / 1e9
         peak, unit = PEAK_HBM_GBS, "GB/s"
-    kernel_name = kernel_instance(stage, workload, layer0, short_max)
+    short_name, long_name = kernel_instance(lib, calls[timed_layers[0]], workload)
+    kernel_name = short_name if stage == "short" else long_name
     roofline = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                 "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(workload.name, kernel_name),
                 "kernel": kernel_name, "kernel_ms": round(kernel_ms, 4), "algorithmic_per_launch": per_launch}

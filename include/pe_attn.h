@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define PE_ATTN_ABI_VERSION 5
+#define PE_ATTN_ABI_VERSION 6
 
 #define PE_ATTN_OK 0
 #define PE_ATTN_EINVAL (-1)       /* malformed arguments (maps to ValueError) */
@@ -95,6 +95,12 @@ typedef struct pe_attn_args {
     const int32_t *cu_seqlens_k;
     int32_t total_tokens_k;
     int32_t max_seqlen_k; /* host bound on every key segment length */
+    /* Kernel for the long segments of a bounded band window each of whose rows spans five
+       32-key blocks (ModernBERT's +-64: floor((31 + right) / 32) + ceil(left / 32) == 4), with
+       head_dim 64, an odd GQA ratio and no cu_seqlens_k: 0 the library's choice (the streaming
+       band kernel from 6144 query tiles of 128 rows x heads, the tiled kernel below), 1 the
+       streaming band kernel, 2 the tiled kernel. Other calls ignore it. */
+    int32_t band_kernel;
 } pe_attn_args;
 
 /* ABI version of the loaded library; callers compare it with PE_ATTN_ABI_VERSION. */
@@ -157,6 +163,18 @@ int pe_packed_short_attn_fwd(const pe_attn_args *args, hipStream_t stream);
    Replaces select_packed_short_attention_config
    (packed_encoders/_kernels/triton_packed_attention.py:29-42). */
 int pe_attn_short_config(int32_t max_seqlen, int32_t head_dim, int32_t out[4]);
+
+/* The kernels pe_varlen_attn_fwd runs for these arguments (host-only, like the workspace
+   size): out[0] the short kernel's key capacity (0: no short kernel), out[1] the long-segment
+   kernel (PE_ATTN_KERNEL_*), out[2] its query tiles per workgroup (strip), out[3] its query
+   rows per tile. No counterpart in the reference; for profiling and tests. */
+#define PE_ATTN_KERNEL_NONE 0
+#define PE_ATTN_KERNEL_TILED 1    /* tiled_attn_kernel: head_dim 64 windowed or causal */
+#define PE_ATTN_KERNEL_GLOBAL64 2 /* global64_attn_kernel: head_dim 64 unbounded */
+#define PE_ATTN_KERNEL_BAND64 3   /* band64_attn_kernel: head_dim 64 streaming band */
+#define PE_ATTN_KERNEL_WIDE 4     /* wide_attn_kernel: head_dim 128 */
+#define PE_ATTN_KERNEL_WIDE16 5   /* wide16_attn_kernel: head_dim 256 */
+int pe_attn_kernels(const pe_attn_args *args, int32_t out[4]);
 
 /* Split-half rotary embedding straight from the packed QKV projection: the producer of the
    layout the attention entry points read (q, k contiguous [n_rows, n_heads, head_dim]; v stays

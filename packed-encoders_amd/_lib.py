@@ -12,11 +12,13 @@ from pathlib import Path
 
 from ._build import LIBRARY
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 DTYPE_BF16 = 1
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, ESCRATCH = 0, -1, -2, -3, -4, -5
 STATIC_SCRATCH_BYTES = 1 << 20  # PE_ATTN_STATIC_SCRATCH_BYTES
+# PE_ATTN_KERNEL_*: the long-segment kernel pe_attn_kernels reports
+KERNEL_NONE, KERNEL_TILED, KERNEL_GLOBAL64, KERNEL_BAND64, KERNEL_WIDE, KERNEL_WIDE16 = range(6)
 
 EXPORTED = (
     "pe_attn_abi_version",
@@ -29,6 +31,7 @@ EXPORTED = (
     "pe_attn_tiled_fwd",
     "pe_packed_short_attn_fwd",
     "pe_attn_short_config",
+    "pe_attn_kernels",
     "pe_rope_qkv_fwd",
 )
 
@@ -70,6 +73,7 @@ class AttnArgs(ctypes.Structure):
         ("cu_seqlens_k", ctypes.c_void_p),
         ("total_tokens_k", ctypes.c_int32),
         ("max_seqlen_k", ctypes.c_int32),
+        ("band_kernel", ctypes.c_int32),
     ]
 
 
@@ -125,6 +129,8 @@ def library(path: str | None = None) -> ctypes.CDLL:
     lib.pe_packed_short_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p]
     lib.pe_attn_short_config.restype = ctypes.c_int
     lib.pe_attn_short_config.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32)]
+    lib.pe_attn_kernels.restype = ctypes.c_int
+    lib.pe_attn_kernels.argtypes = [ctypes.POINTER(AttnArgs), ctypes.POINTER(ctypes.c_int32)]
     lib.pe_rope_qkv_fwd.restype = ctypes.c_int
     lib.pe_rope_qkv_fwd.argtypes = [ctypes.POINTER(RopeArgs), ctypes.c_void_p]
     version = lib.pe_attn_abi_version()

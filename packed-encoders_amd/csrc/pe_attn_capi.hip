@@ -11,6 +11,7 @@
 #include <cstring>
 #include <mutex>
 
+#include "pe_attn_band64.h"
 #include "pe_attn_device.h"
 #include "pe_attn_global64.h"
 #include "pe_attn_plan.h"
@@ -81,6 +82,7 @@ int check_args(const pe_attn_args *a, bool need_pointers = true) {
     if (a->causal != 0 && a->causal != 1) return PE_ATTN_EINVAL;
     if (a->short_max < -1 || a->short_max > 128) return PE_ATTN_EINVAL;
     if (a->strip < 0 || a->strip > kMaxStrip) return PE_ATTN_EINVAL;
+    if (a->band_kernel < 0 || a->band_kernel > 2) return PE_ATTN_EINVAL;
     if (a->cu_seqlens_k && (a->total_tokens_k < 0 || a->max_seqlen_k < 0)) return PE_ATTN_EINVAL;
     if (!need_pointers || a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
     if (!a->q || !a->k || !a->v || !a->o || !a->cu_seqlens) return PE_ATTN_EINVAL;
@@ -137,10 +139,32 @@ int64_t tile_capacity(const pe_attn_args *a, int short_max, int bm, int strip) {
     return by_shape < by_tokens ? by_shape : by_tokens;
 }
 
-// Query tiles per tiled-kernel workgroup: the caller's choice, else the gfx950 default.
+// Query tiles (128 rows x heads) of a call, from host-known sizes.
+int64_t query_tiles(const pe_attn_args *a) { return (int64_t)a->total_tokens / 128 * a->n_heads_q; }
+
+// Whether a call's long segments run the streaming band kernel (band64_attn_kernel) rather than
+// the tiled kernel: its window shape, one query head per kv head group, shared key segments,
+// and the caller's band_kernel choice; by default a call of at least kBandMinTiles query tiles.
+// Measured on gfx950 over C2-like document mixes and equal-length batches (12 heads, +-64):
+// the streaming kernel (two workgroups per CU, long-lived) is 3-13% faster from about 6K
+// tiles up and up to 20% slower on smaller calls, where the tiled kernel's short workgroups
+// (three per CU) balance the tail better.
+constexpr int64_t kBandMinTiles = 6144;
+bool uses_band64(const pe_attn_args *a) {
+    const int wr = a->causal ? 0 : a->window_right;
+    const bool shape = a->head_dim == 64 && !a->cu_seqlens_k && heads_per_tile(a) == 1 &&
+                       pe::band64_window(a->window_left, wr);
+    if (!shape || a->band_kernel == 2) return false;
+    return a->band_kernel == 1 || query_tiles(a) >= kBandMinTiles;
+}
+
+// Query tiles per tiled-kernel workgroup: the caller's choice, else the gfx950 default. The
+// band kernel streams its key blocks along a strip: 4 tiles, 8 on calls of 16K tiles or more
+// (measured best on the same sweep).
 int effective_strip(const pe_attn_args *a) {
     if (a->strip > 0) return a->strip;
-    return 1;
+    if (!uses_band64(a)) return 1;
+    return query_tiles(a) >= 16384 ? 8 : 4;
 }
 
 AttnParams make_params(const pe_attn_args *a, int short_max) {
@@ -173,6 +197,7 @@ AttnParams make_params(const pe_attn_args *a, int short_max) {
     p.max_seqlen = a->max_seqlen;
     p.max_seqlen_k = a->cu_seqlens_k ? a->max_seqlen_k : a->max_seqlen;
     p.strip = effective_strip(a);
+    p.band = uses_band64(a) ? 1 : 0;
     p.c = a->softmax_scale * pe::kLog2e;
     return p;
 }
@@ -256,6 +281,12 @@ int launch_tiled_t(AttnParams p, int64_t cap, hipStream_t stream) {
     if (blocks > 0x7fffffffLL) return PE_ATTN_EUNSUPPORTED;
     if constexpr (D == 64 && !WIN)
         hipLaunchKernelGGL((pe::global64_attn_kernel<G, GATE>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+    else if constexpr (D == 64 && G == 1)
+        if (p.band)
+            hipLaunchKernelGGL((pe::band64_attn_kernel<GATE>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, NS, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0,
+                               stream, p);
     else if constexpr (D == 64)
         hipLaunchKernelGGL((pe::tiled_attn_kernel<D, G, BN, NS, GATE, WIN>), dim3((unsigned)blocks), dim3(256), 0,
                            stream, p);
@@ -439,6 +470,30 @@ int pe_attn_short_config(int32_t max_seqlen, int32_t head_dim, int32_t out[4]) {
     out[1] = sk;
     out[2] = hpw;
     out[3] = 4;
+    return PE_ATTN_OK;
+}
+
+int pe_attn_kernels(const pe_attn_args *a, int32_t out[4]) {
+    int rc = check_args(a, false);
+    if (rc) return rc;
+    if (!out) return PE_ATTN_EINVAL;
+    const int sm = effective_short_max(a);
+    int sk = 0, hpw = 0;
+    if (sm > 0) short_shape(sm, a->head_dim, &sk, &hpw);
+    const int g = heads_per_tile(a);
+    const int32_t max_k = a->cu_seqlens_k ? a->max_seqlen_k : a->max_seqlen;
+    const bool tiled = a->n_seq > 0 && a->total_tokens > 0 && (a->max_seqlen > sm || max_k > sm);
+    int kernel = PE_ATTN_KERNEL_NONE;
+    if (tiled) {
+        if (a->head_dim == 256) kernel = PE_ATTN_KERNEL_WIDE16;
+        else if (a->head_dim == 128) kernel = PE_ATTN_KERNEL_WIDE;
+        else if (global64(a)) kernel = PE_ATTN_KERNEL_GLOBAL64;
+        else kernel = uses_band64(a) ? PE_ATTN_KERNEL_BAND64 : PE_ATTN_KERNEL_TILED;
+    }
+    out[0] = sk;
+    out[1] = kernel;
+    out[2] = tiled ? effective_strip(a) : 0;
+    out[3] = tiled ? tile_rows(a, g) : 0;
     return PE_ATTN_OK;
 }
 

@@ -44,6 +44,7 @@ struct AttnParams {
     int32_t max_seqlen_k;  // and on key segment lengths
     int32_t hgroups; // head groups per work entry (tiled kernel)
     int32_t strip;   // query tiles per work entry (tiled kernel)
+    int32_t band;    // 1: windowed head_dim 64 calls run the streaming band kernel
     float c;         // softmax_scale * log2(e)
     const int4 *work;          // tiled kernels: (segment, first q-tile, query start, query rows)
     const int32_t *work_count; // tiled kernels: number of valid entries

@@ -1,0 +1,164 @@
+"""GPU parity and invariants of the streaming band kernel (band64_attn_kernel), forced with
+``band_kernel=1`` at sizes the library would otherwise give the tiled kernel.
+
+It serves head_dim 64 windows whose rows each span five 32-key blocks (ModernBERT's +-64 and
+any (left, right) in [33, 64] x [33, 64]), one query head per kv head group. Checked: the
+oracle on segment lengths straddling every block and tile edge, MHA and GQA 3:1, the fused
+gate, strips of 1..8 tiles bit-identical to each other, a stale running maximum past the
+overflow guard, zero cross-segment leakage and independence from batch composition (bit for
+bit), and agreement with the tiled kernel within the bf16 tolerance.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from test_hip_attention import WINDOW_LENGTHS, _assert_parity, _dev, _inputs, _oracle
+
+pytestmark = pytest.mark.gpu
+
+BAND_WINDOWS = [(64, 64), (33, 33), (40, 60), (64, 33)]
+
+
+def _kernel_of(q, k, cu, max_seqlen, window, band_kernel):
+    import ctypes
+
+    from packed_encoders_amd import _lib, hip_attention as hip
+
+    out = torch.empty_like(q)
+    a = hip._args(q, k, k, out, cu, max_seqlen, 0.125, window[0], window[1], False, None, 0,
+                  band_kernel=band_kernel)
+    res = (ctypes.c_int32 * 4)()
+    assert _lib.library().pe_attn_kernels(ctypes.byref(a), res) == 0
+    return res[1], res[2]
+
+
+def _run(pe, q, k, v, cu, mx, window, band_kernel=1, gate=None, strip=None):
+    if strip is None:
+        with torch.inference_mode():
+            return pe.varlen_attention(q, k, v, cu, mx, softmax_scale=0.125, window=window, short_max=0,
+                                       gate=gate, band_kernel=band_kernel)
+    import ctypes
+
+    from packed_encoders_amd import _lib, hip_attention as hip
+
+    lib = _lib.library()
+    out = torch.empty_like(q)
+    a = hip._args(q, k, v, out, cu, mx, 0.125, window[0], window[1], False, gate, 0, strip=strip,
+                  band_kernel=band_kernel)
+    size = ctypes.c_size_t()
+    assert lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size)) == 0
+    ws = torch.empty(max(size.value, 1), dtype=torch.uint8, device="cuda")
+    assert lib.pe_varlen_attn_fwd(ctypes.byref(a), ws.data_ptr(), size.value,
+                                  torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (6, 2)], ids=["mha", "gqa3"])
+@pytest.mark.parametrize("window", BAND_WINDOWS, ids=[f"{w[0]}_{w[1]}" for w in BAND_WINDOWS])
+def test_band_kernel_matches_oracle_and_strips_agree(pe, window, hq, hkv):
+    from packed_encoders_amd import _lib
+
+    announce(f"band kernel window={window} heads={hq}/{hkv}")
+    q, k, v, cu, _ = _inputs(WINDOW_LENGTHS, hq=hq, hkv=hkv, seed=61)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    mx = max(WINDOW_LENGTHS)
+    assert _kernel_of(qd, kd, cud, mx, window, 1)[0] == _lib.KERNEL_BAND64
+    got = _run(pe, qd, kd, vd, cud, mx, window)
+    torch.cuda.synchronize()
+    want = _oracle(q, k, v, cu, scale=0.125, window=window)
+    _assert_parity(got, want, cu)
+    for strip in (1, 2, 3, 8):
+        assert torch.equal(_run(pe, qd, kd, vd, cud, mx, window, strip=strip), got), strip
+
+
+def test_band_kernel_gate_and_agreement_with_tiled(pe):
+    from packed_encoders_amd import _lib
+
+    lengths = [2000, 129, 1, 640, 3000, 77]
+    announce("band kernel gate vs tiled")
+    q, k, v, cu, gt = _inputs(lengths, hq=12, seed=62, gate=True)
+    qd, kd, vd, cud, gd = _dev(q, k, v, cu, gt)
+    mx = max(lengths)
+    assert _kernel_of(qd, kd, cud, mx, (64, 64), 2)[0] == _lib.KERNEL_TILED
+    band = _run(pe, qd, kd, vd, cud, mx, (64, 64), gate=gd)
+    tiled = _run(pe, qd, kd, vd, cud, mx, (64, 64), band_kernel=2, gate=gd)
+    torch.cuda.synchronize()
+    want = _oracle(q, k, v, cu, scale=0.125, window=(64, 64), gate=gt)
+    _assert_parity(band, want, cu)
+    _assert_parity(tiled, want, cu)
+    assert (band.float() - tiled.float()).abs().max().item() <= 2e-2
+
+
+@pytest.mark.parametrize("jump", [4.0, 10.0], ids=["below-guard", "past-guard"])
+def test_band_kernel_scores_jumping_past_a_stale_maximum(pe, jump):
+    lengths = [700, 300, 129]
+    announce(f"band kernel score jump={jump}")
+    q, k, v, cu, _ = _inputs(lengths, hq=4, seed=63)
+    q = q.float().abs().bfloat16()
+    k = k.float()
+    for a in (0, 700):
+        k[a + 200:a + 264] = jump
+    k = k.bfloat16()
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    got = _run(pe, qd, kd, vd, cud, max(lengths), (64, 64))
+    torch.cuda.synchronize()
+    want = _oracle(q, k, v, cu, scale=0.125, window=(64, 64))
+    _assert_parity(got, want, cu)
+
+
+def test_band_kernel_no_leakage_and_batch_independence(pe):
+    """Scaling one segment's q/k/v leaves every other segment's bits unchanged; each segment run
+    alone (the band kernel pinned) gives the bits it has inside the batch."""
+    lengths = [300, 1, 257, 1024, 96, 513]
+    announce("band kernel leakage / independence")
+    q, k, v, cu, gt = _inputs(lengths, hq=6, hkv=2, seed=64, gate=True)
+    qd, kd, vd, cud, gd = _dev(q, k, v, cu, gt)
+    mx = max(lengths)
+    base = _run(pe, qd, kd, vd, cud, mx, (64, 64), gate=gd)
+    c = cu.tolist()
+    s = 3
+    q2, k2, v2, g2 = qd.clone(), kd.clone(), vd.clone(), gd.clone()
+    q2[c[s]:c[s + 1]] *= 7
+    k2[c[s]:c[s + 1]] *= 100
+    v2[c[s]:c[s + 1]] *= -100
+    g2[c[s]:c[s + 1]] *= -3
+    changed = _run(pe, q2, k2, v2, cud, mx, (64, 64), gate=g2)
+    torch.cuda.synchronize()
+    assert torch.isfinite(base).all()
+    assert torch.equal(base[:c[s]], changed[:c[s]]) and torch.equal(base[c[s + 1]:], changed[c[s + 1]:])
+    assert not torch.equal(base[c[s]:c[s + 1]], changed[c[s]:c[s + 1]])
+    for i, (a, b) in enumerate(zip(c, c[1:])):
+        cu1 = torch.tensor([0, b - a], dtype=torch.int32, device="cuda")
+        alone = _run(pe, qd[a:b].contiguous(), kd[a:b].contiguous(), vd[a:b].contiguous(), cu1, b - a, (64, 64),
+                     gate=gd[a:b].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(alone, base[a:b]), f"segment {i} ({b - a} rows) differs alone"
+
+
+def test_library_choice_by_call_size(pe):
+    """band_kernel=0 keeps the tiled kernel on a small call and takes the band kernel on a
+    large one; the large call matches the oracle on sampled rows."""
+    from oracle import attention as oa
+    from packed_encoders_amd import _lib
+
+    announce("band kernel size rule")
+    small = [512] * 8
+    q, k, v, cu, _ = _inputs(small, hq=12, seed=65)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    assert _kernel_of(qd, kd, cud, 512, (64, 64), 0)[0] == _lib.KERNEL_TILED
+    big = [4096] * 16  # 512 query tiles x 12 heads = 6144
+    q, k, v, cu, _ = _inputs(big, hq=12, seed=66)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    assert _kernel_of(qd, kd, cud, 4096, (64, 64), 0) == (_lib.KERNEL_BAND64, 4)
+    got = _run(pe, qd, kd, vd, cud, 4096, (64, 64), band_kernel=0)
+    torch.cuda.synchronize()
+    rows = np.linspace(0, sum(big) - 1, 96).astype(np.int64)
+    f = lambda t: t.float().numpy()
+    want = oa.sampled_rows_attention(f(q), f(k), f(v), cu.numpy(), rows, scale=0.125, window=(64, 64), causal=False)
+    err = np.abs(got.float().cpu().numpy()[rows] - want).max()
+    assert err <= 2e-2, err

@@ -54,7 +54,7 @@ def test_library_holds_gfx950_code():
 
 
 def test_abi_version_and_status_text(lib):
-    assert lib.pe_attn_abi_version() == 5
+    assert lib.pe_attn_abi_version() == 6
     assert lib.pe_attn_strerror(0) == b"ok"
     assert lib.pe_attn_strerror(-3) == b"workspace missing or too small"
     assert lib.pe_attn_strerror(-99) == b"unknown status"
@@ -113,7 +113,7 @@ def test_workspace_size_is_host_arithmetic(lib):
 @pytest.mark.parametrize("field,value,status", [
     ("struct_size", 8, -1), ("dtype", 7, -2), ("head_dim", 96, -2), ("n_heads_kv", 5, -1),
     ("softmax_scale", 0.0, -1), ("window_left", -2, -1), ("causal", 2, -1), ("short_max", 129, -1),
-    ("strip", 65, -1), ("strip", -1, -1),
+    ("strip", 65, -1), ("strip", -1, -1), ("band_kernel", 3, -1), ("band_kernel", -1, -1),
 ])
 def test_bad_arguments_are_rejected_before_any_launch(lib, field, value, status):
     rc, _ = _ws(lib, _args(**{field: value}))
@@ -222,3 +222,47 @@ def test_noalloc_entry_point_rejects_calls_past_its_static_scratch(lib):
     # malformed arguments are still reported as such
     assert lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(_args(head_dim=96)), None) == -2
     assert lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(_args(n_seq=0, total_tokens=0)), None) == 0
+
+
+def _kernels(lib, **kw):
+    out = (ctypes.c_int32 * 4)()
+    a = _args(**kw)
+    rc = lib.pe_attn_kernels(ctypes.byref(a), out)
+    assert rc == 0, rc
+    return tuple(out)
+
+
+def test_kernel_choice_per_call(lib):
+    """pe_attn_kernels reports (short capacity, long-segment kernel, strip, tile rows): the
+    global head_dim 64 kernel, the tiled kernel for small band calls and the streaming band
+    kernel from 6144 query tiles (strip 4, 8 from 16384), band_kernel overriding the size
+    rule only where the window shape, an odd GQA ratio and shared key segments allow it."""
+    from packed_encoders_amd import _lib
+
+    band = dict(window_left=64, window_right=64)
+    assert _kernels(lib) == (64, _lib.KERNEL_GLOBAL64, 1, 256)
+    assert _kernels(lib, **band) == (64, _lib.KERNEL_TILED, 1, 128)  # C2: 3041 tiles
+    assert _kernels(lib, band_kernel=1, **band) == (64, _lib.KERNEL_BAND64, 4, 128)
+    c4 = dict(n_seq=16, total_tokens=131072, max_seqlen=8192, n_heads_q=16, n_heads_kv=16)
+    assert _kernels(lib, **c4, **band) == (64, _lib.KERNEL_BAND64, 8, 128)  # 16384 tiles
+    assert _kernels(lib, **c4, band_kernel=2, **band) == (64, _lib.KERNEL_TILED, 1, 128)
+    mid = dict(n_seq=128, total_tokens=67493, max_seqlen=4000)  # 6327 tiles
+    assert _kernels(lib, **mid, **band) == (64, _lib.KERNEL_BAND64, 4, 128)
+    assert _kernels(lib, band_kernel=1, n_heads_q=12, n_heads_kv=4, **band)[1] == _lib.KERNEL_BAND64  # GQA 3:1
+    assert _kernels(lib, band_kernel=1, n_heads_q=12, n_heads_kv=6, **band)[1] == _lib.KERNEL_TILED  # GQA 2:1
+    assert _kernels(lib, band_kernel=1, window_left=5, window_right=7)[1] == _lib.KERNEL_TILED
+    assert _kernels(lib, band_kernel=1, window_left=33, window_right=64)[1] == _lib.KERNEL_BAND64
+    assert _kernels(lib, band_kernel=1, window_left=64, window_right=-1, causal=1)[1] == _lib.KERNEL_TILED
+    assert _kernels(lib, head_dim=128) == (32, _lib.KERNEL_WIDE, 1, 128)
+    assert _kernels(lib, head_dim=256, n_heads_q=8, n_heads_kv=2) == (0, _lib.KERNEL_WIDE16, 1, 16)
+    assert _kernels(lib, max_seqlen=64, **band) == (64, _lib.KERNEL_NONE, 0, 0)
+    a = _args(band_kernel=1, **band)
+    a.cu_seqlens_k = 8  # sizes only
+    a.total_tokens_k, a.max_seqlen_k = 32438, 2048
+    out = (ctypes.c_int32 * 4)()
+    assert lib.pe_attn_kernels(ctypes.byref(a), out) == 0 and out[1] == _lib.KERNEL_TILED
+    # the band kernel's strips size the workspace: 4 tiles of 128 rows per entry
+    rc, size = _ws(lib, _args(band_kernel=1, **band))
+    n_long = min(64, 32438 // 65)
+    tiles = (32438 + n_long * 127) // 128
+    assert rc == 0 and size == 256 + 16 * min(64 * 4, (tiles + n_long * 3) // 4)
