@@ -22,8 +22,12 @@ For C2 the line also carries ``end_to_end``: the whole packed ModernBERT-base fo
 (random-init weights, bf16) over the same batch through ``pe.pack``, eager and replayed from
 the bucketed HIP-graph runner, in tokens/s.
 
+Before the W warm-up steps the step runs untimed for ``--settle`` seconds (0.3 by default,
+reported as ``settle_s``): an idle MI355X measures up to 10% slower over its first ~10 ms of
+load, which a 20-step timed region of a sub-millisecond step would otherwise include.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C2] [--no-cpu-baseline]
-                       [--no-model]
+                       [--no-model] [--settle S]
 """
 
 from __future__ import annotations
@@ -141,6 +145,23 @@ def kernel_instance(lib, call, workload):
     return short, long
 
 
+def settle(step, seconds: float) -> float:
+    """Run `step` untimed until `seconds` of wall time have passed (synchronising every few
+    steps); returns the time spent. An idle MI355X reaches its sustained clock and memory
+    behaviour only after some load: the first ~10 ms of a kernel stream measure up to 10% slower
+    than the same kernels a few hundred milliseconds in (measured on the band kernel: 303 us
+    cold against 266-273 us warm for the same launch). Settling first makes a short timed
+    region report the steady state a continuously serving process sees."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(4):
+            step()
+        torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
 def gpu_bench(args, workload):
     import torch
 
@@ -192,6 +213,7 @@ def gpu_bench(args, workload):
                 bracket(c.tiled, events, sp) if here and stage == "tiled" else c.tiled(sp)
 
     timed = []
+    settle_s = settle(step, args.settle)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -257,7 +279,7 @@ def gpu_bench(args, workload):
         "tokens_per_s": round(workload.total_tokens / (graph_ms * 1e-3), 1)}
     return {
         "value": value, "ms_per_step": wall_ms, "gpu_ms_per_step": gpu_ms, "flops_per_step": flops,
-        "graph_replay": replay,
+        "graph_replay": replay, "settle_s": round(settle_s, 3),
         "tokens_per_s": workload.total_tokens / (wall_ms * 1e-3), "roofline": roofline, "short_max": short_max,
         "_outputs": (calls, cu),
     }
@@ -313,6 +335,7 @@ def model_bench(args, workload):
     stream = torch.cuda.current_stream(dev)
 
     def timed(fn):
+        settle(fn, args.settle)
         for _ in range(max(args.warmup, 2)):
             fn()
         torch.cuda.synchronize()
@@ -506,7 +529,7 @@ def profile_commands(out: str = "gpurun_out/prof") -> list[tuple[str, str]]:
         run = f"python3 bench.py --workload {w} --no-cpu-baseline --no-model"
         cmds.append((f"{w}_kt", f"rocprofv3 --kernel-trace --stats --output-format csv -d {out}/{w}_kt -o k -- "
                                 f"{run} --steps 10 --warmup 2"))
-        run += " --no-graph"  # counter passes: eager launches only
+        run += " --no-graph --settle 0.05"  # counter passes: eager launches, short settle
         for pmc in ("FETCH_SIZE", "WRITE_SIZE"):
             cmds.append((f"{w}_{pmc}", f"rocprofv3 --pmc {pmc} --output-format csv -d {out}/{w}_{pmc} -o p -- "
                                        f"{run} --steps 2 --warmup 1"))
@@ -746,6 +769,8 @@ def main() -> int:
     ap.add_argument("--strip", type=int, default=0, help="query tiles per tiled-kernel workgroup (0: library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the graph-replayed timing of the step")
+    ap.add_argument("--settle", type=float, default=0.3,
+                    help="seconds of untimed steps before the warm-up, to reach the sustained clock (default 0.3)")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the end-to-end packed ModernBERT forward (C2 only)")
     ap.add_argument("--dispatch-sweep", action="store_true",
@@ -825,6 +850,7 @@ def main() -> int:
         "tokens_per_s": round(res["tokens_per_s"], 1),
         "gpu_ms_per_step": round(res["gpu_ms_per_step"], 4),
         "graph_replay": res["graph_replay"],
+        "settle_s": res["settle_s"],
         "roofline": res["roofline"],
         "cpu_baseline": cpu_res,
     }

@@ -54,18 +54,6 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
-// Wait until at most n vector memory operations are outstanding (n wave-uniform), rounded
-// down to one of the counts below: a smaller count only waits longer.
-__device__ __forceinline__ void wait_vmcnt_at_most(int n) {
-    if (n >= 16) wait_vmcnt<16>();
-    else if (n >= 12) wait_vmcnt<12>();
-    else if (n >= 8) wait_vmcnt<8>();
-    else if (n >= 6) wait_vmcnt<6>();
-    else if (n >= 4) wait_vmcnt<4>();
-    else if (n >= 2) wait_vmcnt<2>();
-    else wait_vmcnt<0>();
-}
-
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const PE_LDS void *)p;
 }
