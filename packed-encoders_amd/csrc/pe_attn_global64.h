@@ -1,6 +1,7 @@
 // Packed global (bidirectional, unwindowed) attention for long segments, head_dim 64, on
 // gfx950 MFMA: the MFMA-bound layers of a packed encoder batch (ModernBERT's global layers,
-// long documents). Windowed and causal calls run tiled_attn_kernel (pe_attn_tiled.h).
+// long documents). Windowed and causal calls run tiled_attn_kernel (pe_attn_tiled.h) or, for
+// large calls with a +-64-shaped band, band64_attn_kernel (pe_attn_band64.h).
 //
 // Work shape. One workgroup = 4 waves = one strip of query tiles of one segment for a group of
 // G query heads sharing a kv head. Each wave owns 64 query rows of one head, held in VGPRs as

@@ -1,6 +1,8 @@
-// Tiled flash-style packed attention for long segments, head_dim 64 (gfx950 MFMA); wider
-// heads use wide_attn_kernel (head_dim 128, pe_attn_tiled_wide.h) and wide16_attn_kernel
-// (head_dim 256, pe_attn_tiled_wide16.h), which share the staging below.
+// Tiled flash-style packed attention for long segments, head_dim 64 (gfx950 MFMA): windowed and
+// causal calls (global calls run global64_attn_kernel, pe_attn_global64.h; large calls with a
+// +-64-shaped band the streaming band64_attn_kernel, pe_attn_band64.h). Wider heads use
+// wide_attn_kernel (head_dim 128, pe_attn_tiled_wide.h) and wide16_attn_kernel (head_dim 256,
+// pe_attn_tiled_wide16.h), which share the staging below.
 //
 // One workgroup = 4 waves = one strip of consecutive query tiles of one segment, for one group
 // of G query heads. A query tile has 32*4/G rows: the G heads share one kv head (G divides the
