@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import hashlib
 import os
+import re
 import shutil
 import subprocess
 from pathlib import Path
@@ -35,13 +36,22 @@ HIPCC_FLAGS = [
 SOURCES = ["pe_attn_capi.hip"]
 
 
+def _code_only(text: str) -> str:
+    """C/C++ source with comments removed and whitespace collapsed (no string literal in these
+    sources holds a comment marker)."""
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", " ", text)
+    return " ".join(text.split())
+
+
 def source_digest() -> str:
-    """A short sha256 over the library's HIP sources, its public headers and the compile flags:
-    what ties a committed profile of the kernels to the code it measured."""
+    """A short sha256 over the code of the library's HIP sources and public headers (comments
+    and layout excluded) and the compile flags: what ties a committed profile of the kernels to
+    the code it measured."""
     h = hashlib.sha256(" ".join(HIPCC_FLAGS).encode())
     for path in sorted(p for p in [*CSRC.iterdir(), *INCLUDE.iterdir()] if p.is_file()):
         h.update(path.name.encode())
-        h.update(path.read_bytes())
+        h.update(_code_only(path.read_text()).encode())
     return h.hexdigest()[:16]
 
 
