@@ -515,7 +515,7 @@ SQ_PASSES = {  # two counter passes of at most 8 SQ counters (plus GRBM) each
     "SQB": "SQ_VALU_MFMA_BUSY_CYCLES SQ_VALU_MFMA_COEXEC_CYCLES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS "
            "SQ_WAIT_INST_LDS SQ_LDS_BANK_CONFLICT SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE",
 }
-MFMA_PROFILED = ("C2", "C3", "C4")
+MFMA_PROFILED = ("C2", "C3", "C4", "C4-band", "C5")  # SQ counter passes (MFMA and VALU use, waits)
 
 
 def profile_commands(out: str = "gpurun_out/prof") -> list[tuple[str, str]]:
