@@ -70,13 +70,16 @@ class LayerCall:
     cu_seqlens, the window and the head geometry, so a packed forward builds it once per kind
     (twice for ModernBERT: global and +-64) and every layer of that kind reuses it."""
 
-    def __init__(self, lib, hip, workload, layer, cu, q, k, v, gate, short_max, plans, strip=0):
+    def __init__(self, lib, hip, workload, layer, cu, q, k, v, gate, short_max, plans, strip=0, min_seqlen=True):
         import torch
 
         self.lib, self.layer = lib, layer
         self.out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+        # The host knows the batch's lengths (it built cu_seqlens from them), so it passes the
+        # shortest beside max_seqlen, as a collator does.
+        shortest = min(workload.lengths) if min_seqlen and workload.lengths else 0
         self.args = hip._args(q, k, v, self.out, cu, workload.max_seqlen, workload.scale, layer.window[0],
-                              layer.window[1], layer.causal, gate, short_max, strip)
+                              layer.window[1], layer.causal, gate, short_max, strip, min_seqlen=shortest)
         size = ctypes.c_size_t()
         rc = lib.pe_attn_workspace_size(ctypes.byref(self.args), ctypes.byref(size))
         assert rc == 0, rc
@@ -185,7 +188,8 @@ def gpu_bench(args, workload):
         k = torch.randn(T, hkv, d, device=dev, generator=gen, dtype=torch.bfloat16)
         v = torch.randn(T, hkv, d, device=dev, generator=gen, dtype=torch.bfloat16)
         g = torch.randn(T, hq, d, device=dev, generator=gen, dtype=torch.bfloat16) if layer.gate else None
-        calls.append(LayerCall(lib, hip, workload, layer, cu, q, k, v, g, short_max, plans, args.strip))
+        calls.append(LayerCall(lib, hip, workload, layer, cu, q, k, v, g, short_max, plans, args.strip,
+                               not args.no_min_seqlen))
     stage, bound, timed_layers = dominant(workload, short_max)
     stream = torch.cuda.current_stream(dev)
 
@@ -281,6 +285,7 @@ def gpu_bench(args, workload):
         "value": value, "ms_per_step": wall_ms, "gpu_ms_per_step": gpu_ms, "flops_per_step": flops,
         "graph_replay": replay, "settle_s": round(settle_s, 3),
         "tokens_per_s": workload.total_tokens / (wall_ms * 1e-3), "roofline": roofline, "short_max": short_max,
+        "min_seqlen": int(calls[0].args.min_seqlen),
         "_outputs": (calls, cu),
     }
 
@@ -767,6 +772,8 @@ def main() -> int:
     ap.add_argument("--workload", default="C2", help="C1 C2 C3 C4 C4-band C5 Q4096 (default C2)")
     ap.add_argument("--short-max", type=int, default=None, help="routing boundary (default: gfx950 policy)")
     ap.add_argument("--strip", type=int, default=0, help="query tiles per tiled-kernel workgroup (0: library default)")
+    ap.add_argument("--no-min-seqlen", action="store_true",
+                    help="pass no lower bound on the segment lengths (the short pass then always launches)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the graph-replayed timing of the step")
     ap.add_argument("--settle", type=float, default=0.3,
@@ -845,6 +852,7 @@ def main() -> int:
             "attention_layers": len(workload.layers),
             "global_layers": n_global,
             "short_max": res["short_max"],
+            "min_seqlen": res["min_seqlen"],
             "parallelism": "single GPU",
         },
         "tokens_per_s": round(res["tokens_per_s"], 1),

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define PE_ATTN_ABI_VERSION 6
+#define PE_ATTN_ABI_VERSION 7
 
 #define PE_ATTN_OK 0
 #define PE_ATTN_EINVAL (-1)       /* malformed arguments (maps to ValueError) */
@@ -101,6 +101,13 @@ typedef struct pe_attn_args {
        band kernel from 6144 query tiles of 128 rows x heads, the tiled kernel below), 1 the
        streaming band kernel, 2 the tiled kernel. Other calls ignore it. */
     int32_t band_kernel;
+    /* Host lower bound on every query segment length, or 0 when not known (flash_attn's
+       varlen interface carries max_seqlen only; a collator that packs host-known lengths
+       knows both). When it exceeds the routing boundary no segment can take the short
+       kernel: pe_attn_short_fwd launches nothing and the plan gives every segment to the
+       tiled kernels, which serve any length, so a bound that is wrong costs time, never
+       results. 0 <= min_seqlen <= max_seqlen. */
+    int32_t min_seqlen;
 } pe_attn_args;
 
 /* ABI version of the loaded library; callers compare it with PE_ATTN_ABI_VERSION. */
@@ -110,7 +117,8 @@ int pe_attn_abi_version(void);
 const char *pe_attn_strerror(int status);
 
 /* Bytes of device workspace pe_varlen_attn_fwd needs for these arguments (host-only, from
-   n_seq, total_tokens, max_seqlen, head geometry and short_max; never reads device memory). */
+   n_seq, total_tokens, max_seqlen, min_seqlen, head geometry and short_max; never reads
+   device memory). */
 int pe_attn_workspace_size(const pe_attn_args *args, size_t *bytes);
 
 /* Packed varlen attention, both kernels in one call. Segments are routed per segment on the
@@ -138,7 +146,8 @@ int pe_varlen_attn_fwd_noalloc(const pe_attn_args *args, hipStream_t stream);
 /* The three stages pe_varlen_attn_fwd runs, for callers that reuse one plan across calls
    (the 22 layers of a packed forward share cu_seqlens: one plan per window kind serves all
    of them) or time one kernel. A plan is valid for arguments with the same cu_seqlens
-   contents, n_seq, total_tokens, max_seqlen, head counts, window, causal and short_max.
+   contents, n_seq, total_tokens, max_seqlen, min_seqlen, head counts, window, causal and
+   short_max.
    pe_attn_plan: build the cost-ordered (segment, query tile) list of the tiled kernel into
      the workspace (no-op when no segment can exceed short_max). The workspace starts with two
      int32 words: the entries written and the entries needed. They differ only when the

@@ -12,7 +12,7 @@ from pathlib import Path
 
 from ._build import LIBRARY
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 DTYPE_BF16 = 1
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, ESCRATCH = 0, -1, -2, -3, -4, -5
@@ -74,6 +74,7 @@ class AttnArgs(ctypes.Structure):
         ("total_tokens_k", ctypes.c_int32),
         ("max_seqlen_k", ctypes.c_int32),
         ("band_kernel", ctypes.c_int32),
+        ("min_seqlen", ctypes.c_int32),
     ]
 
 

@@ -83,6 +83,7 @@ int check_args(const pe_attn_args *a, bool need_pointers = true) {
     if (a->short_max < -1 || a->short_max > 128) return PE_ATTN_EINVAL;
     if (a->strip < 0 || a->strip > kMaxStrip) return PE_ATTN_EINVAL;
     if (a->band_kernel < 0 || a->band_kernel > 2) return PE_ATTN_EINVAL;
+    if (a->min_seqlen < 0 || a->min_seqlen > a->max_seqlen) return PE_ATTN_EINVAL;
     if (a->cu_seqlens_k && (a->total_tokens_k < 0 || a->max_seqlen_k < 0)) return PE_ATTN_EINVAL;
     if (!need_pointers || a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
     if (!a->q || !a->k || !a->v || !a->o || !a->cu_seqlens) return PE_ATTN_EINVAL;
@@ -114,11 +115,18 @@ int check_args(const pe_attn_args *a, bool need_pointers = true) {
     return PE_ATTN_OK;
 }
 
-int effective_short_max(const pe_attn_args *a) {
+int routing_boundary(const pe_attn_args *a) {
     if (a->head_dim > 128) return 0;  // the short kernel covers head_dim <= 128
     if (a->short_max >= 0) return a->short_max;
     const int32_t longest = a->cu_seqlens_k && a->max_seqlen_k > a->max_seqlen ? a->max_seqlen_k : a->max_seqlen;
     return longest > 0 && longest <= kShortCapacity ? longest : default_boundary(a->head_dim);
+}
+
+// The boundary a call routes by: 0 (every segment to the tiled kernels) when the caller's
+// lower bound on the lengths leaves no segment short, which spares the short pass's launch.
+int effective_short_max(const pe_attn_args *a) {
+    const int sm = routing_boundary(a);
+    return a->min_seqlen > sm ? 0 : sm;
 }
 
 int heads_per_tile(const pe_attn_args *a) { return gcd_int(a->n_heads_q / a->n_heads_kv, 4); }

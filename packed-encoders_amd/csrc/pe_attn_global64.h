@@ -161,30 +161,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     const float c2 = p.c;
 
-    // Loader: the next step to stage, NS - 1 steps ahead of the consumer; void steps (zeros,
-    // no memory traffic) past the strip's end keep every step's load count equal.
+    // Loader: the next step to stage, NS - 1 steps ahead of the consumer; nothing past the
+    // strip's last step. n_issued / n_begun count the steps staged and begun (wave-uniform).
     int ld_qt = qt_first, ld_t = -2;
+    int n_issued = 0, n_begun = 0;
     auto issue_next = [&](int stage) {
-        if (ld_qt < qt_end) {
-            if (ld_t < 0) issue_q(stage, ld_qt, ld_t + 2);
-            else issue_kv(stage, ld_t * BN);
-            if (++ld_t >= nkt) {
-                ++ld_qt;
-                ld_t = -2;
-            }
-        } else {
-            const uint32_t kb = ring_base + stage * kStageBytes + wave * 2048;
-            const uint32_t lds[4] = {kb, kb + 1024, kb + kTileBytes, kb + kTileBytes + 1024};
-            const int off[4] = {kVoidOffset, kVoidOffset, kVoidOffset, kVoidOffset};
-            dma16x4(lds, off, k_rs, k_rs);
+        if (ld_qt >= qt_end) return;
+        ++n_issued;
+        if (ld_t < 0) issue_q(stage, ld_qt, ld_t + 2);
+        else issue_kv(stage, ld_t * BN);
+        if (++ld_t >= nkt) {
+            ++ld_qt;
+            ld_t = -2;
         }
     };
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) issue_next(st);
 
+    // A step's loads are complete once at most the following step's LPS loads are in flight
+    // (loads complete in issue order; outstanding output stores only make the wait stricter),
+    // or none when no following step was staged: the strip's last step leaves no load in
+    // flight, so the workgroup ends without draining its output stores.
     int stage = 0;
     auto begin_step = [&]() {
-        wait_vmcnt<(NS - 2) * LPS>();
+        if (n_issued > n_begun + 1) wait_vmcnt<(NS - 2) * LPS>();
+        else wait_vmcnt<0>();
+        ++n_begun;
         __syncthreads();
         issue_next(stage == 0 ? NS - 1 : stage - 1);
     };
@@ -450,8 +452,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             }
         }
     }
-    // Loads of void steps may still be landing in LDS: drain before the workgroup ends.
-    wait_vmcnt<0>();
 }
 
 }  // namespace pe

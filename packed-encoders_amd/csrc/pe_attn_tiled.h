@@ -24,8 +24,8 @@
 // The ring carries one flat sequence of steps: for each query tile of the strip, 64 / BN "Q
 // steps" that bring the tile's query rows into a stage (each wave reads its 32 rows from there
 // into registers), then one step per key tile. Every step loads the same number of 16-byte
-// units per lane, and past the strip's end the loader issues void steps (out-of-range loads:
-// zeros, no memory traffic), so "this step's loads are done" is one constant s_waitcnt vmcnt.
+// units per lane, so "this step's loads are done" is one constant s_waitcnt vmcnt (vmcnt 0 for
+// the strip's last step, after which nothing is staged).
 // No load the compiler can see remains in the loop (only the gate's), so it never inserts a
 // vector-memory wait of its own that would drain the ring. Every global access goes through a
 // buffer resource bounded by the segment, so rows past the segment read as zero with no
@@ -226,31 +226,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
 
     const float c2 = p.c;
 
-    // Loader: the next step to stage, walked NS - 1 steps ahead of the consumer. Past the
-    // strip's last step it stages "void" steps (out-of-range buffer loads: zeros, no memory
-    // traffic) so that every step issues the same number of loads and the wait below is one
-    // constant count.
+    // Loader: the next step to stage, walked NS - 1 steps ahead of the consumer; nothing past
+    // the strip's last step. n_issued / n_begun count the steps staged and begun (wave-uniform).
     int ld_qt = qt_first, ld_t = -QS, ld_klo, ld_nt;
     key_range(ld_qt, ld_klo, ld_nt);
+    int n_issued = 0, n_begun = 0;
     auto issue_next = [&](int stage) {
-        if (ld_qt < qt_end) {
-            if (ld_t < 0) issue_q(stage, ld_qt, ld_t + QS);
-            else issue_kv(stage, ld_klo + ld_t * BN);
-            if (++ld_t >= ld_nt) {
-                ++ld_qt;
-                ld_t = -QS;
-                if (ld_qt < qt_end) key_range(ld_qt, ld_klo, ld_nt);
-            }
-        } else {
-            const uint32_t kb = ring_base + stage * kStageBytes + wave * UPW * 1024;
-            uint32_t lds[LPS];
-            int off[LPS];
-#pragma unroll
-            for (int j = 0; j < LPS; ++j) {
-                lds[j] = kb + (j % UPW) * 1024 + (j / UPW) * kTileBytes;
-                off[j] = kVoidOffset;
-            }
-            dma_step(lds, off, k_rs, k_rs);
+        if (ld_qt >= qt_end) return;
+        ++n_issued;
+        if (ld_t < 0) issue_q(stage, ld_qt, ld_t + QS);
+        else issue_kv(stage, ld_klo + ld_t * BN);
+        if (++ld_t >= ld_nt) {
+            ++ld_qt;
+            ld_t = -QS;
+            if (ld_qt < qt_end) key_range(ld_qt, ld_klo, ld_nt);
         }
     };
 #pragma unroll
@@ -262,10 +251,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
     int stage = 0;  // ring stage of the current step
     // Start of a step: its loads are complete once at most the NS - 2 later steps' loads are in
     // flight (loads complete in issue order; other outstanding accesses only make the wait
-    // stricter); after the barrier every wave is done with the previous step's stage, which is
-    // refilled with the step NS - 1 ahead.
+    // stricter), or none when no later step was staged, so the strip's last step leaves no load
+    // in flight and the workgroup ends without draining its output stores. After the barrier
+    // every wave is done with the previous step's stage, which is refilled with the step NS - 1
+    // ahead.
     auto begin_step = [&]() {
-        wait_vmcnt<(NS - 2) * LPS>();
+        if (n_issued > n_begun + 1) wait_vmcnt<(NS - 2) * LPS>();
+        else wait_vmcnt<0>();
+        ++n_begun;
         __syncthreads();
         issue_next(stage == 0 ? NS - 1 : stage - 1);
     };
@@ -432,8 +425,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
             store_block<DB, GATE>(o, inv, kg, o_rs, ooff, g_rs, goff);
         }
     }
-    // Loads of void steps may still be landing in LDS: drain before the workgroup ends.
-    wait_vmcnt<0>();
 }
 
 }  // namespace pe

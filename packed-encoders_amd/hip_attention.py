@@ -40,7 +40,7 @@ def _aligned(t: Tensor) -> Tensor:
 def _args(q: Tensor, k: Tensor, v: Tensor, o: Tensor, cu: Tensor, max_seqlen: int, scale: float,
           window_left: int, window_right: int, causal: bool, gate: Tensor | None,
           short_max: int, strip: int = 0, cu_k: Tensor | None = None,
-          max_seqlen_k: int = 0, band_kernel: int = 0) -> _lib.AttnArgs:
+          max_seqlen_k: int = 0, band_kernel: int = 0, min_seqlen: int = 0) -> _lib.AttnArgs:
     a = _lib.AttnArgs()
     a.struct_size = ctypes.sizeof(_lib.AttnArgs)
     a.dtype = _lib.DTYPE_BF16
@@ -63,6 +63,7 @@ def _args(q: Tensor, k: Tensor, v: Tensor, o: Tensor, cu: Tensor, max_seqlen: in
     a.short_max = int(short_max)
     a.strip = int(strip)
     a.band_kernel = int(band_kernel)
+    a.min_seqlen = int(min_seqlen)
     if cu_k is not None:
         a.cu_seqlens_k = cu_k.data_ptr()
         a.total_tokens_k = k.shape[0]
@@ -119,13 +120,13 @@ def _plan_key(args: _lib.AttnArgs, cu: Tensor, cu_k: Tensor | None = None) -> tu
     kv = (None,) if cu_k is None else (id(cu_k), cu_k.data_ptr(), args.total_tokens_k, args.max_seqlen_k)
     return (id(cu), cu.data_ptr(), cu.numel(), args.total_tokens, args.max_seqlen, args.n_heads_q,
             args.n_heads_kv, args.head_dim, args.window_left, args.window_right, args.causal, args.short_max,
-            args.strip, args.band_kernel, *kv)
+            args.strip, args.band_kernel, args.min_seqlen, *kv)
 
 
 def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int,
                  softmax_scale: float, window_left: int, window_right: int, causal: bool,
                  gate: Tensor | None, short_max: int, cu_seqlens_k: Tensor | None = None,
-                 max_seqlen_k: int = 0, band_kernel: int = 0) -> Tensor:
+                 max_seqlen_k: int = 0, band_kernel: int = 0, min_seqlen: int = 0) -> Tensor:
     _check_tensors(q, k, v, cu_seqlens, gate, cu_seqlens_k)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     gate = _aligned(gate) if gate is not None else None
@@ -134,7 +135,8 @@ def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen
         return out
     lib = _lib.library()
     args = _args(q, k, v, out, cu_seqlens, max_seqlen, softmax_scale, window_left, window_right,
-                 causal, gate, short_max, cu_k=cu_seqlens_k, max_seqlen_k=max_seqlen_k, band_kernel=band_kernel)
+                 causal, gate, short_max, cu_k=cu_seqlens_k, max_seqlen_k=max_seqlen_k, band_kernel=band_kernel,
+                 min_seqlen=min_seqlen)
     stream = torch.cuda.current_stream(q.device).cuda_stream
     plans = _PLANS.get()
     if plans is None:
@@ -178,17 +180,17 @@ def _short_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen:
 
 def _varlen_op_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int, softmax_scale: float,
                     window_left: int, window_right: int, causal: bool, gate: Tensor | None, short_max: int,
-                    band_kernel: int = 0) -> Tensor:
+                    band_kernel: int = 0, min_seqlen: int = 0) -> Tensor:
     return _varlen_impl(q, k, v, cu_seqlens, max_seqlen, softmax_scale, window_left, window_right, causal, gate,
-                        short_max, band_kernel=band_kernel)
+                        short_max, band_kernel=band_kernel, min_seqlen=min_seqlen)
 
 
 def _varlen_kv_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens_q: Tensor, cu_seqlens_k: Tensor,
                     max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float, window_left: int,
                     window_right: int, causal: bool, gate: Tensor | None, short_max: int,
-                    band_kernel: int = 0) -> Tensor:
+                    band_kernel: int = 0, min_seqlen: int = 0) -> Tensor:
     return _varlen_impl(q, k, v, cu_seqlens_q, max_seqlen_q, softmax_scale, window_left, window_right, causal,
-                        gate, short_max, cu_seqlens_k, max_seqlen_k, band_kernel)
+                        gate, short_max, cu_seqlens_k, max_seqlen_k, band_kernel, min_seqlen)
 
 
 def _meta(q: Tensor, *args, **kwargs) -> Tensor:
@@ -241,13 +243,13 @@ def _register() -> None:
     try:
         lib.define("varlen_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, int max_seqlen, "
                    "float softmax_scale, int window_left, int window_right, bool causal, Tensor? gate, "
-                   "int short_max, int band_kernel=0) -> Tensor")
+                   "int short_max, int band_kernel=0, int min_seqlen=0) -> Tensor")
         lib.define("packed_short_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, int max_seqlen, "
                    "float softmax_scale, int window_left, int window_right) -> Tensor")
         lib.define("rope_qkv(Tensor qkv, Tensor cos, Tensor sin, int h, int d) -> Tensor[]")
         lib.define("varlen_attention_kv(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
                    "int max_seqlen_q, int max_seqlen_k, float softmax_scale, int window_left, int window_right, "
-                   "bool causal, Tensor? gate, int short_max, int band_kernel=0) -> Tensor")
+                   "bool causal, Tensor? gate, int short_max, int band_kernel=0, int min_seqlen=0) -> Tensor")
     except RuntimeError:
         return  # already defined by an earlier import in this process
     lib.impl("varlen_attention", _varlen_op_impl, "CUDA")
@@ -268,7 +270,8 @@ def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_se
                      softmax_scale: float | None = None, window: tuple[int, int] = (-1, -1),
                      causal: bool = False, gate: Tensor | None = None,
                      short_max: int | None = None, cu_seqlens_k: Tensor | None = None,
-                     max_seqlen_k: int | None = None, band_kernel: int = 0) -> Tensor:
+                     max_seqlen_k: int | None = None, band_kernel: int = 0,
+                     min_seqlen: int | None = None) -> Tensor:
     """Packed varlen attention: q ``[T, Hq, D]``, k/v ``[T, Hkv, D]`` bf16, int32 ``cu_seqlens``.
 
     ``window=(left, right)`` bounds ``i - j <= left`` and ``j - i <= right`` (-1 unbounded,
@@ -287,9 +290,18 @@ def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_se
     ``band_kernel`` picks the kernel of a +-64-shaped band call's long segments (see
     ``pe_attn_args.band_kernel``): 0 the library's choice by call size, 1 the streaming band
     kernel, 2 the tiled kernel; results agree within bf16 rounding, not bit for bit.
+
+    ``min_seqlen`` is an optional host lower bound on the query segment lengths (a collator
+    that packs host-known lengths has it beside ``max_seqlen``). When it exceeds the routing
+    boundary no segment can be short, and the call skips the short kernel's launch: every
+    segment goes to the tiled kernels, which serve any length, so a wrong bound costs time,
+    never results.
     """
     if band_kernel not in (0, 1, 2):
         raise ValueError("band_kernel must be 0 (library choice), 1 (streaming band) or 2 (tiled)")
+    min_seqlen = 0 if min_seqlen is None else int(min_seqlen)
+    if not 0 <= min_seqlen <= int(max_seqlen):
+        raise ValueError(f"min_seqlen must lie in [0, max_seqlen], got {min_seqlen} (max_seqlen {max_seqlen})")
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
         raise ValueError("the HIP packed attention is forward-only; call it under torch.no_grad()")
     scale = q.shape[-1] ** -0.5 if softmax_scale is None else float(softmax_scale)
@@ -300,10 +312,11 @@ def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_se
             raise ValueError("cu_seqlens_k needs max_seqlen_k")
         return torch.ops.pe_hip.varlen_attention_kv(q, k, v, cu_seqlens, cu_seqlens_k, int(max_seqlen),
                                                     int(max_seqlen_k), scale, int(window[0]), int(window[1]),
-                                                    bool(causal), gate, int(short_max), int(band_kernel))
+                                                    bool(causal), gate, int(short_max), int(band_kernel),
+                                                    min_seqlen)
     return torch.ops.pe_hip.varlen_attention(q, k, v, cu_seqlens, int(max_seqlen), scale,
                                              int(window[0]), int(window[1]), bool(causal), gate,
-                                             int(short_max), int(band_kernel))
+                                             int(short_max), int(band_kernel), min_seqlen)
 
 
 def packed_short_attention_supported(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor,

@@ -386,6 +386,35 @@ def test_window_gate_and_short_routing(pe, window, causal):
     _assert_parity(got, want, cu)
 
 
+@pytest.mark.parametrize("window", [(-1, -1), (64, 64)], ids=["global", "band64"])
+def test_min_seqlen_bound_skips_the_short_pass_only(pe, window):
+    """A lower bound on the lengths above the boundary: with no short segment the output is
+    bit-identical to the unbounded call (same plan, same kernel); with short segments present
+    (a bound that is wrong) the tiled kernel serves them and the output still matches the
+    oracle."""
+    announce(f"min_seqlen bound window={window}")
+    long_only = [98, 300, 129, 1000, 65]
+    q, k, v, cu, gt = _inputs(long_only, hq=4, seed=71, gate=True)
+    qd, kd, vd, cud, gd = _dev(q, k, v, cu, gt)
+    mx = max(long_only)
+    with torch.inference_mode():
+        plain = pe.varlen_attention(qd, kd, vd, cud, mx, softmax_scale=0.125, window=window, gate=gd)
+        bounded = pe.varlen_attention(qd, kd, vd, cud, mx, softmax_scale=0.125, window=window, gate=gd,
+                                      min_seqlen=min(long_only))
+    torch.cuda.synchronize()
+    assert torch.equal(plain, bounded)
+    _assert_parity(bounded, _oracle(q, k, v, cu, scale=0.125, window=window, gate=gt), cu)
+    mixed = [5, 300, 64, 1, 129, 33]
+    q, k, v, cu, _ = _inputs(mixed, hq=4, seed=72)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    with torch.inference_mode():
+        wrong = pe.varlen_attention(qd, kd, vd, cud, max(mixed), softmax_scale=0.125, window=window, min_seqlen=65)
+    torch.cuda.synchronize()
+    _assert_parity(wrong, _oracle(q, k, v, cu, scale=0.125, window=window), cu)
+    with pytest.raises(ValueError):
+        pe.varlen_attention(qd, kd, vd, cud, max(mixed), min_seqlen=max(mixed) + 1)
+
+
 @pytest.mark.parametrize("window,causal", [((-1, -1), False), ((64, 64), False), ((-1, -1), True), ((200, 7), False)],
                          ids=["global", "band64", "causal", "asym"])
 def test_long_segments_planned_by_waves(pe, window, causal):

@@ -54,7 +54,7 @@ def test_library_holds_gfx950_code():
 
 
 def test_abi_version_and_status_text(lib):
-    assert lib.pe_attn_abi_version() == 6
+    assert lib.pe_attn_abi_version() == 7
     assert lib.pe_attn_strerror(0) == b"ok"
     assert lib.pe_attn_strerror(-3) == b"workspace missing or too small"
     assert lib.pe_attn_strerror(-99) == b"unknown status"
@@ -114,6 +114,7 @@ def test_workspace_size_is_host_arithmetic(lib):
     ("struct_size", 8, -1), ("dtype", 7, -2), ("head_dim", 96, -2), ("n_heads_kv", 5, -1),
     ("softmax_scale", 0.0, -1), ("window_left", -2, -1), ("causal", 2, -1), ("short_max", 129, -1),
     ("strip", 65, -1), ("strip", -1, -1), ("band_kernel", 3, -1), ("band_kernel", -1, -1),
+    ("min_seqlen", -1, -1), ("min_seqlen", 2049, -1),
 ])
 def test_bad_arguments_are_rejected_before_any_launch(lib, field, value, status):
     rc, _ = _ws(lib, _args(**{field: value}))
@@ -266,3 +267,20 @@ def test_kernel_choice_per_call(lib):
     n_long = min(64, 32438 // 65)
     tiles = (32438 + n_long * 127) // 128
     assert rc == 0 and size == 256 + 16 * min(64 * 4, (tiles + n_long * 3) // 4)
+
+
+def test_min_seqlen_above_the_boundary_skips_the_short_pass(lib):
+    """A host lower bound on the lengths above the routing boundary leaves no segment short:
+    no short kernel, every segment planned for the tiled kernel (the workspace bound counts
+    all N segments as long); at or below the boundary, or 0 (unknown), routing is unchanged."""
+    from packed_encoders_amd import _lib
+
+    assert _kernels(lib, min_seqlen=98) == (0, _lib.KERNEL_GLOBAL64, 1, 256)
+    assert _kernels(lib, min_seqlen=64) == (64, _lib.KERNEL_GLOBAL64, 1, 256)
+    assert _kernels(lib, min_seqlen=0) == (64, _lib.KERNEL_GLOBAL64, 1, 256)
+    assert _kernels(lib, head_dim=128, min_seqlen=33) == (0, _lib.KERNEL_WIDE, 1, 128)
+    assert _kernels(lib, short_max=100, min_seqlen=98) == (128, _lib.KERNEL_GLOBAL64, 1, 256)  # capacity 128
+    # every segment short by max_seqlen: the bound cannot exceed it, routing stays all-short
+    assert _kernels(lib, max_seqlen=64, min_seqlen=64) == (64, _lib.KERNEL_NONE, 0, 0)
+    rc, size = _ws(lib, _args(min_seqlen=98))
+    assert rc == 0 and size == 256 + 16 * min(64 * 8, (32438 + 64 * 255) // 256)
