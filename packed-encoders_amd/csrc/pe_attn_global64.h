@@ -348,16 +348,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         // groups of the independent softmax VALU work (sched_group_barrier: 0x008 MFMA, 0x002
         // VALU, 0x100 LDS read), so the wave keeps the matrix core fed while it computes
         // probabilities; sched_barrier fences the regions.
-        auto pipelined_tile = [&](const __bf16 *kt, const __bf16 *vt) -> int {
+        auto pipelined_tile = [&](bool first, const __bf16 *kt, const __bf16 *vt) -> int {
             bf16x8 k4[4], v4[2][2], pa[2], pbb[2];
             float st0, st1;
-            // R0: S_A0, S_B0; softmax A0 under S_B0.
+            // R0: S_A0, then S_B0 with softmax A0 under it. A query tile's first key tile seeds
+            // the stale maximum of each half from these scores (half A once S_A0 is done, half
+            // B after the check), a uniform branch at the region's edges.
             load_k(kt, 0, k4);
             f32x16 sa = qk(k4, 0);
-            f32x16 sb = qk(k4, 1);
-            probs(sa, 0, pa, st0, st1);
             __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (first) seed_max(sa, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            f32x16 sb = qk(k4, 1);
+            probs(sa, 0, pa, st0, st1);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -365,6 +370,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             }
             __builtin_amdgcn_sched_barrier(0);
             if (!accept(0, st0, st1)) return 0;
+            if (first) seed_max(sb, 1);
             __builtin_amdgcn_sched_barrier(0);
             // R1: S_A1, O_A += V0 P_A0; softmax B0 under them.
             load_k(kt, 1, k4);
@@ -421,18 +427,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
                 const int kt0 = t * BN;
                 int from = 0;
                 if (kt0 + BN <= Lk) {
-                    if (t == 0) {
-                        // First key tile: the stale maximum seeded from block 0's scores (8
-                        // MFMAs more per query tile; the pipelined schedule itself stays free of
-                        // branches).
-                        bf16x8 k4[4];
-                        load_k(kt, 0, k4);
-                        const f32x16 sa = qk(k4, 0);
-                        const f32x16 sb = qk(k4, 1);
-                        seed_max(sa, 0);
-                        seed_max(sb, 1);
-                    }
-                    from = pipelined_tile(kt, vt);
+                    // A query tile's first key tile seeds the stale maximum from its first
+                    // block's scores inside the pipelined schedule.
+                    from = pipelined_tile(t == 0, kt, vt);
                 }
                 if (from < 4) exact_from(kt, vt, kt0, from);
             }
