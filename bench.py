@@ -119,6 +119,18 @@ def dominant(workload, short_max):
     return "tiled", "hbm", list(range(len(workload.layers)))
 
 
+def useful_flops_served(workload, short_max, kernel):
+    """Useful FLOPs per launch of ``kernel`` (the short kernel or the long-segment kernel of the
+    dominant layer): 4 D Hq sum(allowed pairs) over the segments it serves."""
+    from packed_encoders_amd import hip_attention as hip
+
+    _, _, timed = dominant(workload, short_max)
+    layer = workload.layers[timed[0]]
+    short = kernel.startswith("pe::short_attn_kernel")
+    served = [n for n in workload.lengths if (n <= short_max) == short]
+    return hip.useful_flops(served, workload.n_heads_q, workload.head_dim, window=layer.window, causal=layer.causal)
+
+
 def kernel_instance(lib, call, workload):
     """The name rocprofv3 lists (template arguments included) for the kernels of one layer's
     call, as the library reports its choice (pe_attn_kernels): (short kernel, long kernel)."""
@@ -679,9 +691,9 @@ def summarize_profiles(src: Path) -> int:
                        "| counter | per dispatch |", "|---|---|"]
                 for c in sorted(m):
                     out.append(f"| {c} | {m[c]:,.0f} |")
+                useful = useful_flops_served(wl, bench_line["config"]["short_max"], roof["kernel"])
                 out += ["", "| derived | value |", "|---|---|",
-                        f"| MFMA FLOPs (MOPS_BF16 x 512) | {flops:.4g} (algorithmic "
-                        f"{roof['algorithmic_per_launch']:.4g}) |",
+                        f"| MFMA FLOPs (MOPS_BF16 x 512) | {flops:.4g} (useful {useful:.4g}) |",
                         f"| MFMA pipe busy / (4 SIMDs x SQ_BUSY_CU_CYCLES) | "
                         f"{m['SQ_VALU_MFMA_BUSY_CYCLES'] / (4 * m['SQ_BUSY_CU_CYCLES']):.3f} |",
                         f"| MFMA pipe busy / (1024 SIMDs x GRBM_GUI_ACTIVE / 8) | "
@@ -695,7 +707,10 @@ def summarize_profiles(src: Path) -> int:
                         f"| LDS bank conflicts / LDS instructions | "
                         f"{m['SQ_LDS_BANK_CONFLICT'] / m['SQ_INSTS_LDS']:.3f} |",
                         "", f"Event-timed in the bench line of the kernel-trace run: {roof['kernel_ms'] * 1e3:.1f} us, "
-                        f"{roof['achieved']} TFLOP/s = {roof['frac']:.1%} of the 2.5 PFLOP/s dense bf16 peak."]
+                        f"{useful / (roof['kernel_ms'] * 1e-3) / 1e12:.1f} useful TFLOP/s = "
+                        f"{useful / (roof['kernel_ms'] * 1e-3) / 2.5e15:.1%} of the 2.5 PFLOP/s dense bf16 peak; "
+                        f"its roofline ({roof['bound']}-bound): {roof['achieved']} {roof['unit']} = "
+                        f"{roof['frac']:.1%} of {roof['peak']} {roof['unit']}."]
                 (prof / f"{w}_mfma_counters.md").write_text("\n".join(out) + "\n")
     (prof / "traffic.json").write_text(json.dumps(traffic, indent=1, sort_keys=True) + "\n")
     return 0
