@@ -136,7 +136,7 @@ def kernel_instance(lib, call, workload):
     call, as the library reports its choice (pe_attn_kernels): (short kernel, long kernel)."""
     from packed_encoders_amd import _lib
 
-    out = (ctypes.c_int32 * 4)()
+    out = (ctypes.c_int32 * 6)()
     rc = lib.pe_attn_kernels(ctypes.byref(call.args), out)
     if rc:
         raise RuntimeError(f"pe_attn_kernels: {rc}")
@@ -146,9 +146,7 @@ def kernel_instance(lib, call, workload):
     g = math.gcd(workload.n_heads_q // workload.n_heads_kv, 4)
     short = None
     if out[0]:
-        sk = out[0]
-        hpw = (2 if sk == 128 else 4) if d == 64 else (4 if sk == 32 else (2 if sk == 64 else 1))
-        short = f"pe::short_attn_kernel<{d}, {sk}, {hpw}, {gate}>"
+        short = f"pe::short_attn_kernel<{d}, {out[0]}, {out[4]}, {gate}>"
     long = {
         _lib.KERNEL_NONE: None,
         _lib.KERNEL_TILED: f"pe::tiled_attn_kernel<64, {g}, 64, 3, {gate}, {win}>",

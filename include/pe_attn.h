@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define PE_ATTN_ABI_VERSION 7
+#define PE_ATTN_ABI_VERSION 8
 
 #define PE_ATTN_OK 0
 #define PE_ATTN_EINVAL (-1)       /* malformed arguments (maps to ValueError) */
@@ -176,14 +176,16 @@ int pe_attn_short_config(int32_t max_seqlen, int32_t head_dim, int32_t out[4]);
 /* The kernels pe_varlen_attn_fwd runs for these arguments (host-only, like the workspace
    size): out[0] the short kernel's key capacity (0: no short kernel), out[1] the long-segment
    kernel (PE_ATTN_KERNEL_*), out[2] its query tiles per workgroup (strip), out[3] its query
-   rows per tile. No counterpart in the reference; for profiling and tests. */
+   rows per tile, out[4] the short kernel's query heads per workgroup (fewer than
+   pe_attn_short_config's when the batch would leave CUs idle) and out[5] its workgroups.
+   No counterpart in the reference; for profiling and tests. */
 #define PE_ATTN_KERNEL_NONE 0
 #define PE_ATTN_KERNEL_TILED 1    /* tiled_attn_kernel: head_dim 64 windowed or causal */
 #define PE_ATTN_KERNEL_GLOBAL64 2 /* global64_attn_kernel: head_dim 64 unbounded */
 #define PE_ATTN_KERNEL_BAND64 3   /* band64_attn_kernel: head_dim 64 streaming band */
 #define PE_ATTN_KERNEL_WIDE 4     /* wide_attn_kernel: head_dim 128 */
 #define PE_ATTN_KERNEL_WIDE16 5   /* wide16_attn_kernel: head_dim 256 */
-int pe_attn_kernels(const pe_attn_args *args, int32_t out[4]);
+int pe_attn_kernels(const pe_attn_args *args, int32_t out[6]);
 
 /* Split-half rotary embedding straight from the packed QKV projection: the producer of the
    layout the attention entry points read (q, k contiguous [n_rows, n_heads, head_dim]; v stays

@@ -12,7 +12,7 @@ from pathlib import Path
 
 from ._build import LIBRARY
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 DTYPE_BF16 = 1
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, ESCRATCH = 0, -1, -2, -3, -4, -5

@@ -217,6 +217,9 @@ int launch_short_t(const AttnParams &p, hipStream_t stream) {
     return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
 }
 
+// Compute units of an MI355X.
+constexpr int64_t kCUs = 256;
+
 // Static short-kernel choice: key capacity SK (32/64/128) and heads per workgroup, sized so
 // the workgroup's K and V^T stay within ~75 KB of LDS (two workgroups per CU).
 void short_shape(int max_len, int d, int *sk, int *hpw) {
@@ -227,24 +230,37 @@ void short_shape(int max_len, int d, int *sk, int *hpw) {
         *hpw = *sk == 32 ? 4 : (*sk == 64 ? 2 : 1);
 }
 
+// hpw never exceeds the shape's default (short_shape), the most heads whose K and V fit LDS.
+template <int D, int SK, bool GATE>
+int launch_short_h(const AttnParams &p, int hpw, hipStream_t stream) {
+    constexpr int kMax = (D == 64 ? 4 : 2) * 64 / SK;  // short_shape's hpw (4, 4, 2 / 4, 2, 1)
+    if constexpr (kMax >= 4)
+        if (hpw == 4) return launch_short_t<D, SK, 4, GATE>(p, stream);
+    if constexpr (kMax >= 2)
+        if (hpw == 2) return launch_short_t<D, SK, 2, GATE>(p, stream);
+    return launch_short_t<D, SK, 1, GATE>(p, stream);
+}
+
 template <int D, bool GATE>
-int launch_short_d(const AttnParams &p, int sk, hipStream_t stream) {
-    if constexpr (D == 64) {
-        if (sk == 32) return launch_short_t<D, 32, 4, GATE>(p, stream);
-        if (sk == 64) return launch_short_t<D, 64, 4, GATE>(p, stream);
-        return launch_short_t<D, 128, 2, GATE>(p, stream);
-    } else {
-        if (sk == 32) return launch_short_t<D, 32, 4, GATE>(p, stream);
-        if (sk == 64) return launch_short_t<D, 64, 2, GATE>(p, stream);
-        return launch_short_t<D, 128, 1, GATE>(p, stream);
-    }
+int launch_short_d(const AttnParams &p, int sk, int hpw, hipStream_t stream) {
+    if (sk == 32) return launch_short_h<D, 32, GATE>(p, hpw, stream);
+    if (sk == 64) return launch_short_h<D, 64, GATE>(p, hpw, stream);
+    return launch_short_h<D, 128, GATE>(p, hpw, stream);
+}
+
+// Heads per short-kernel workgroup for a call: the shape's default, halved while the call
+// would give fewer than two workgroups per CU (a small batch: more, smaller workgroups).
+int short_heads(int hpw, int64_t n_seq, int hq) {
+    while (hpw > 1 && n_seq * ((hq + hpw - 1) / hpw) < 2 * kCUs) hpw /= 2;
+    return hpw;
 }
 
 int launch_short(const AttnParams &p, int d, bool gate, int short_max, hipStream_t stream) {
     int sk, hpw;
     short_shape(short_max, d, &sk, &hpw);
-    if (d == 64) return gate ? launch_short_d<64, true>(p, sk, stream) : launch_short_d<64, false>(p, sk, stream);
-    if (d == 128) return gate ? launch_short_d<128, true>(p, sk, stream) : launch_short_d<128, false>(p, sk, stream);
+    hpw = short_heads(hpw, p.n_seq, p.hq);
+    if (d == 64) return gate ? launch_short_d<64, true>(p, sk, hpw, stream) : launch_short_d<64, false>(p, sk, hpw, stream);
+    if (d == 128) return gate ? launch_short_d<128, true>(p, sk, hpw, stream) : launch_short_d<128, false>(p, sk, hpw, stream);
     return PE_ATTN_EUNSUPPORTED;
 }
 
@@ -481,7 +497,7 @@ int pe_attn_short_config(int32_t max_seqlen, int32_t head_dim, int32_t out[4]) {
     return PE_ATTN_OK;
 }
 
-int pe_attn_kernels(const pe_attn_args *a, int32_t out[4]) {
+int pe_attn_kernels(const pe_attn_args *a, int32_t out[6]) {
     int rc = check_args(a, false);
     if (rc) return rc;
     if (!out) return PE_ATTN_EINVAL;
@@ -502,6 +518,10 @@ int pe_attn_kernels(const pe_attn_args *a, int32_t out[4]) {
     out[1] = kernel;
     out[2] = tiled ? effective_strip(a) : 0;
     out[3] = tiled ? tile_rows(a, g) : 0;
+    const int heads = sk ? short_heads(hpw, a->n_seq, a->n_heads_q) : 0;
+    const int64_t groups = heads ? (int64_t)a->n_seq * ((a->n_heads_q + heads - 1) / heads) : 0;
+    out[4] = heads;
+    out[5] = (int32_t)(groups < 0x7fffffff ? groups : 0x7fffffff);
     return PE_ATTN_OK;
 }
 

@@ -31,7 +31,7 @@ def _kernel_of(q, k, cu, max_seqlen, window, band_kernel):
     out = torch.empty_like(q)
     a = hip._args(q, k, k, out, cu, max_seqlen, 0.125, window[0], window[1], False, None, 0,
                   band_kernel=band_kernel)
-    res = (ctypes.c_int32 * 4)()
+    res = (ctypes.c_int32 * 6)()
     assert _lib.library().pe_attn_kernels(ctypes.byref(a), res) == 0
     return res[1], res[2]
 

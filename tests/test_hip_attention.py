@@ -89,6 +89,36 @@ def test_packed_short_attention_matches_oracle(pe, lengths, half_window):
     assert mean < 4e-3
 
 
+SHORT_HEADS = [(64, 12, 32, 1), (64, 12, 100, 2), (64, 12, 200, 4), (128, 6, 40, 1), (128, 6, 200, 2)]
+
+
+@pytest.mark.parametrize("d,hq,n_seq,heads", SHORT_HEADS, ids=[f"d{c[0]}_{c[2]}seg" for c in SHORT_HEADS])
+def test_short_kernel_heads_per_workgroup(pe, d, hq, n_seq, heads):
+    """A small batch runs the short kernel with fewer query heads per workgroup (the library
+    reports the choice, pe_attn_kernels out[4]): every choice matches the oracle with the gate
+    and a +-16 window over lengths 1..64, and the first 32 segments run alone (one head per
+    workgroup) are bit-identical to the same segments inside the larger batch."""
+    from packed_encoders_amd import _lib
+    from packed_encoders_amd.hip_attention import _args
+
+    announce(f"short kernel d={d} hq={hq} n_seq={n_seq} heads={heads}")
+    rng = np.random.default_rng(n_seq + d)
+    lengths = rng.integers(1, 65, size=n_seq).tolist()
+    q, k, v, cu, gt = _inputs(lengths, hq=hq, d=d, seed=n_seq, gate=True)
+    qd, kd, vd, cud, gd = _dev(q, k, v, cu, gt)
+    lib = _lib.library()
+    out = (ctypes.c_int32 * 6)()
+    a = _args(qd, kd, vd, qd, cud, 64, 0.125, 16, 16, False, gd, 64, 0)
+    assert lib.pe_attn_kernels(ctypes.byref(a), out) == 0
+    assert (out[0], out[1], out[4], out[5]) == (64, _lib.KERNEL_NONE, heads, n_seq * -(-hq // heads))
+    got = _launch(lib, qd, kd, vd, cud, 64, (16, 16), False, gate=gd, short_max=64)
+    want = _oracle(q, k, v, cu, scale=0.125, window=(16, 16), gate=gt)
+    _assert_parity(got, want, cu)
+    t32 = int(cu[32])
+    alone = _launch(lib, qd[:t32], kd[:t32], vd[:t32], cud[:33], 64, (16, 16), False, gate=gd[:t32], short_max=64)
+    assert torch.equal(alone, got[:t32])
+
+
 LONG_CASES = [
     ([1, 300, 1000, 129, 2048, 64, 7], (-1, -1), False),
     ([1, 300, 1000, 129, 2048, 64, 7], (64, 64), False),

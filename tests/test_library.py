@@ -54,7 +54,7 @@ def test_library_holds_gfx950_code():
 
 
 def test_abi_version_and_status_text(lib):
-    assert lib.pe_attn_abi_version() == 7
+    assert lib.pe_attn_abi_version() == 8
     assert lib.pe_attn_strerror(0) == b"ok"
     assert lib.pe_attn_strerror(-3) == b"workspace missing or too small"
     assert lib.pe_attn_strerror(-99) == b"unknown status"
@@ -225,12 +225,27 @@ def test_noalloc_entry_point_rejects_calls_past_its_static_scratch(lib):
     assert lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(_args(n_seq=0, total_tokens=0)), None) == 0
 
 
-def _kernels(lib, **kw):
-    out = (ctypes.c_int32 * 4)()
+def _kernels(lib, short=False, **kw):
+    out = (ctypes.c_int32 * 6)()
     a = _args(**kw)
     rc = lib.pe_attn_kernels(ctypes.byref(a), out)
     assert rc == 0, rc
-    return tuple(out)
+    return tuple(out)[4:] if short else tuple(out)[:4]
+
+
+def test_short_kernel_heads_per_workgroup(lib):
+    """pe_attn_kernels reports the short kernel's heads per workgroup and its workgroups: the
+    shape's default (pe_attn_short_config) halved while the batch would give fewer than two
+    workgroups per CU (512 on 256 CUs), so a small batch spreads over more CUs."""
+    q = dict(max_seqlen=64, total_tokens=1307)
+    assert _kernels(lib, short=True, n_seq=32, **q) == (1, 32 * 12)  # C1
+    assert _kernels(lib, short=True, n_seq=100, **q) == (2, 100 * 6)
+    assert _kernels(lib, short=True, n_seq=171, **q) == (4, 171 * 3)
+    assert _kernels(lib, short=True, n_seq=4096, max_seqlen=64, total_tokens=164139) == (4, 4096 * 3)  # Q4096
+    assert _kernels(lib, short=True, n_seq=300, max_seqlen=128, total_tokens=20000) == (2, 300 * 6)
+    assert _kernels(lib, short=True, head_dim=128, n_seq=4096, max_seqlen=128, total_tokens=300000) == (1, 4096 * 12)
+    assert _kernels(lib, short=True, head_dim=128, n_seq=40, max_seqlen=32, total_tokens=800) == (1, 40 * 12)
+    assert _kernels(lib, short=True, head_dim=256, n_heads_q=8, n_heads_kv=2) == (0, 0)
 
 
 def test_kernel_choice_per_call(lib):
@@ -260,7 +275,7 @@ def test_kernel_choice_per_call(lib):
     a = _args(band_kernel=1, **band)
     a.cu_seqlens_k = 8  # sizes only
     a.total_tokens_k, a.max_seqlen_k = 32438, 2048
-    out = (ctypes.c_int32 * 4)()
+    out = (ctypes.c_int32 * 6)()
     assert lib.pe_attn_kernels(ctypes.byref(a), out) == 0 and out[1] == _lib.KERNEL_TILED
     # the band kernel's strips size the workspace: 4 tiles of 128 rows per entry
     rc, size = _ws(lib, _args(band_kernel=1, **band))
