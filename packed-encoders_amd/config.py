@@ -71,27 +71,34 @@ class ModernBertParams:
 
 
 def global_every(config) -> int:
-    """The global-layer period. transformers 5 stores the schedule as ``layer_types``; the
-    period is recovered from it and must describe "global at layers 0, n, 2n, ..."."""
+    """The global-layer period n: layers 0, n, 2n, ... are global. transformers 5 keeps only
+    the ``layer_types`` list; n is then the position of the second global layer (the layer
+    count when layer 0 is the only one), and the list must be exactly that pattern."""
     kinds = getattr(config, "layer_types", None)
     if not kinds:
         return int(config.global_attn_every_n_layers)
     kinds = list(kinds)
-    if set(kinds) <= {"full_attention", "sliding_attention"}:
-        for period in range(1, len(kinds) + 1):
-            if all((kind == "full_attention") == (i % period == 0) for i, kind in enumerate(kinds)):
-                return period
+    at = [i for i, kind in enumerate(kinds) if kind == "full_attention"]
+    known = set(kinds) <= {"full_attention", "sliding_attention"}
+    if known and at and at[0] == 0:
+        n = at[1] if len(at) > 1 else len(kinds)
+        if at == list(range(0, len(kinds), n)):
+            return n
     raise ValueError(f"global attention must recur every n layers from layer 0; got layer_types={kinds}")
 
 
 def rope_thetas(config) -> tuple[float, float]:
-    """(global, local) RoPE base for either config schema."""
-    global_theta = getattr(config, "global_rope_theta", None)
-    local_theta = getattr(config, "local_rope_theta", None)
-    if global_theta is None or local_theta is None:
-        params = getattr(config, "rope_parameters", None)
-        params = params if isinstance(params, dict) else {}
-        fallback = getattr(config, "rope_theta", None) or 160_000.0
-        global_theta = global_theta or params.get("full_attention", {}).get("rope_theta") or fallback
-        local_theta = local_theta or params.get("sliding_attention", {}).get("rope_theta") or fallback
-    return float(global_theta), float(local_theta)
+    """(global, local) RoPE bases. Each is the 4.x field (``global_rope_theta``,
+    ``local_rope_theta``) when the config has it, else the ``rope_theta`` of its layer kind in
+    the 5.x ``rope_parameters``, else ``rope_theta``, else ModernBERT's 160,000."""
+    per_kind = getattr(config, "rope_parameters", None)
+    per_kind = per_kind if isinstance(per_kind, dict) else {}
+    default = getattr(config, "rope_theta", None) or 160_000.0
+
+    def base(field: str, kind: str) -> float:
+        value = getattr(config, field, None)
+        if value is None:
+            value = (per_kind.get(kind) or {}).get("rope_theta") or default
+        return float(value)
+
+    return base("global_rope_theta", "full_attention"), base("local_rope_theta", "sliding_attention")

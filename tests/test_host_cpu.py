@@ -71,6 +71,34 @@ def test_config_schema_variants():
         ModernBertParams.from_hf_config(NotBert)
 
 
+def test_global_period_is_the_smallest_period_of_layer_types():
+    """global_every against a brute-force search over every full/sliding pattern of up to 8
+    layers: the smallest n with "layer i is global iff i % n == 0", and ValueError when none is."""
+    import itertools
+    from types import SimpleNamespace
+
+    for n_layers in range(1, 9):
+        for bits in itertools.product((False, True), repeat=n_layers):
+            kinds = ["full_attention" if b else "sliding_attention" for b in bits]
+            want = next((n for n in range(1, n_layers + 1) if all(b == (i % n == 0) for i, b in enumerate(bits))),
+                        None)
+            cfg = SimpleNamespace(layer_types=kinds)
+            if want is None:
+                with pytest.raises(ValueError):
+                    global_every(cfg)
+            else:
+                assert global_every(cfg) == want, kinds
+
+
+def test_rope_bases_per_field_and_schema():
+    from types import SimpleNamespace as NS
+
+    assert rope_thetas(NS(global_rope_theta=1.0, local_rope_theta=None,
+                          rope_parameters={"sliding_attention": {"rope_theta": 2.0}})) == (1.0, 2.0)
+    assert rope_thetas(NS(rope_parameters={"full_attention": {"rope_theta": 3.0}}, rope_theta=4.0)) == (3.0, 4.0)
+    assert rope_thetas(NS()) == (160_000.0, 160_000.0)
+
+
 # ----------------------------------------------------------------------------- unpad / repad
 
 
