@@ -35,6 +35,25 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// Store two 4-dim bf16 chunks per lane of the 16x16 accumulator layout as 16 contiguous bytes:
+// x holds the lane's chunk of block 2j, y of block 2j + 1 (rows g4 = lane / 16 of 16 lanes).
+// v_permlane32_swap exchanges rows 2-3 of x with rows 0-1 of y, then v_permlane16_swap rows
+// 1 and 3 of x with rows 0 and 2 of y; row g4 then holds, in (x, y), the chunks of lanes
+// (2 (g4 % 2), 2 (g4 % 2) + 1) of block 2j + g4 / 2, and stores them at byte 16 g4.
+__device__ __forceinline__ void store16_pair(__amdgpu_buffer_rsrc_t r, int voff, bf16x4 x, bf16x4 y) {
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 a = __builtin_bit_cast(u32x2, x), b = __builtin_bit_cast(u32x2, y);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const auto s32 = __builtin_amdgcn_permlane32_swap(a[k], b[k], false, false);
+        const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
+        a[k] = s16[0];
+        b[k] = s16[1];
+    }
+    const i32x4 v = {(int)a[0], (int)a[1], (int)b[0], (int)b[1]};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, 0);
+}
+
 // Run length of the XCD dealing for NW waves per workgroup and an NS-stage ring of 32 KB
 // stages: the workgroups 32 CUs hold at once (LDS allows 160 KB / ring per CU, registers two
 // waves per SIMD).
@@ -308,13 +327,21 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
             lt += __shfl_xor(lt, 16);
             lt += __shfl_xor(lt, 32);
             if (wave_active) {
+                // Lane (c16, g4) rounds its 4-dim chunks (16 db + 4 g4 ..), then for each pair of
+                // 16-dim blocks (2j, 2j + 1) a 32-lane and a 16-lane swap regroup the four lanes
+                // of a row so that lane g4 holds dims 16 (2j + g4 / 2) + 8 (g4 % 2) .. + 7:
+                // 16 contiguous bytes at 64 j + 16 g4, one store per pair instead of two.
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-                const int ooff = myrow * (int)p.o_st * 2 + 8 * g4;
+                const int ooff = myrow * (int)p.o_st * 2 + 16 * g4;
 #pragma unroll
-                for (int db = 0; db < DB; ++db)
-                    buf_st8(o_rs, ooff + 32 * db,
-                            round4<GATE>(o[db][0] * inv, o[db][1] * inv, o[db][2] * inv, o[db][3] * inv,
-                                         sgv[GATE ? db : 0]));
+                for (int j = 0; j < DB / 2; ++j) {
+                    const bf16x4 y0 = round4<GATE>(o[2 * j][0] * inv, o[2 * j][1] * inv, o[2 * j][2] * inv,
+                                                   o[2 * j][3] * inv, sgv[GATE ? 2 * j : 0]);
+                    const bf16x4 y1 = round4<GATE>(o[2 * j + 1][0] * inv, o[2 * j + 1][1] * inv,
+                                                   o[2 * j + 1][2] * inv, o[2 * j + 1][3] * inv,
+                                                   sgv[GATE ? 2 * j + 1 : 0]);
+                    store16_pair(o_rs, ooff + 64 * j, y0, y1);
+                }
             }
             reset();
             if (qt + 1 >= qt_end) break;
