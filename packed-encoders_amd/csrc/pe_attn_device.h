@@ -241,66 +241,65 @@ __device__ __forceinline__ bf16x4 round4(float a0, float a1, float a2, float a3,
     }
 }
 
-// round4 of 4 outputs with the gate's sigmoid taken here from its 4 raw values g (GATE).
-template <bool GATE>
-__device__ __forceinline__ bf16x4 out4(float a0, float a1, float a2, float a3, bf16x4 g) {
-    if constexpr (!GATE) return round4<false>(a0, a1, a2, a3, g);
-    else return round4<true>(a0, a1, a2, a3, sigmoid4(g));
+__device__ __forceinline__ bf16x8 buf_ld16_g(__amdgpu_buffer_rsrc_t r, int voff) { return buf_ld16(r, voff, 0); }
+__device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t r, int voff, bf16x8 x) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), r, voff, 0, 0);
 }
 
-// Epilogue of a wave's query block: NCH chunks of 4 consecutive dims of the lane's query row,
-// chunk c holding vals(c) (unnormalised) for dims dim0(c) .. dim0(c) + 3. Scales by inv,
-// applies the optional gate and stores 8 bytes per chunk. Gate loads go out in batches of 8
-// chunks, two batches in flight: batch b + 1 is waited for after batch b's stores are issued
-// (so the wait does not include them) and batch b + 2 is issued next, into b's registers.
-// Only the first batch's latency is exposed; a load next to each use would wait once per
-// chunk, and each such wait would also cover every store before it.
-template <int NCH, bool GATE, class Vals, class Dim0>
-__device__ __forceinline__ void store_chunks(Vals vals, Dim0 dim0, float inv, __amdgpu_buffer_rsrc_t o_rs, int ooff,
-                                             __amdgpu_buffer_rsrc_t g_rs, int goff) {
-    auto chunk = [&](int c, bf16x4 g4) {
-        const f32x4 v = vals(c);
-        buf_st8(o_rs, ooff + dim0(c) * 2, out4<GATE>(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv, g4));
-    };
-    if constexpr (!GATE) {
+// Two rounded 4-dim chunks of one query row, x held by lanes (col, kg) for dims d + 4 kg and y
+// for dims d + 8 + 4 kg, regrouped by one v_permlane32_swap per dword (x's lanes 32-63 with
+// y's lanes 0-31) into 8 contiguous dims per lane: d + 8 kg .. + 7.
+__device__ __forceinline__ bf16x8 swap32_pair(bf16x4 x, bf16x4 y) {
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 a = __builtin_bit_cast(u32x2, x), b = __builtin_bit_cast(u32x2, y);
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) chunk(c, bf16x4{});
-    } else {
-        static_assert(NCH % 8 == 0, "gate batches are 8 chunks");
-        constexpr int NBATCH = NCH / 8;
-        bf16x4 g[2][8];
-        auto load = [&](int b, bf16x4 (&gb)[8]) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) gb[c] = buf_ld8(g_rs, goff + dim0(8 * b + c) * 2, 0);
-        };
-        auto force = [&](bf16x4 (&gb)[8]) {
-            asm volatile("" : "+v"(gb[0]), "+v"(gb[1]), "+v"(gb[2]), "+v"(gb[3]), "+v"(gb[4]), "+v"(gb[5]),
-                         "+v"(gb[6]), "+v"(gb[7]));
-        };
-        load(0, g[0]);
-        if (NBATCH > 1) load(1, g[1]);
-        force(g[0]);
-#pragma unroll
-        for (int b = 0; b < NBATCH; ++b) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) chunk(8 * b + c, g[b & 1][c]);
-            if (b + 1 < NBATCH) force(g[(b + 1) & 1]);
-            if (b + 2 < NBATCH) load(b + 2, g[b & 1]);
-        }
+    for (int k = 0; k < 2; ++k) {
+        const auto s = __builtin_amdgcn_permlane32_swap(a[k], b[k], false, false);
+        a[k] = s[0];
+        b[k] = s[1];
     }
+    const bf16x4 lo = __builtin_bit_cast(bf16x4, a), hi = __builtin_bit_cast(bf16x4, b);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// store_chunks for the 32x32 accumulator layout: lane (col, kg) holds row `col` of O^T in
-// o[db][4 jj + i] = dims 32 db + 8 jj + 4 kg + i.
+// bf16(x * bf16(sigmoid(g))) of 8 outputs x already rounded to bf16 and their 8 raw gate values:
+// with x exact in bf16 this is round4<true>'s bf16(bf16(o) * bf16(sigmoid(g))).
+__device__ __forceinline__ bf16x8 gate8(bf16x8 x, bf16x8 g) {
+    const bf16x4 lo = round4<true>((float)x[0], (float)x[1], (float)x[2], (float)x[3],
+                                   sigmoid4(bf16x4{g[0], g[1], g[2], g[3]}));
+    const bf16x4 hi = round4<true>((float)x[4], (float)x[5], (float)x[6], (float)x[7],
+                                   sigmoid4(bf16x4{g[4], g[5], g[6], g[7]}));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Epilogue of a wave's 32-row query block in the 32x32 accumulator layout: lane (col, kg) holds
+// row `col` of O^T in o[db][4 jj + i] = dims 32 db + 8 jj + 4 kg + i. Scales by inv, rounds to
+// bf16, and for each pair of chunks (jj = 2m, 2m + 1) swaps halves with the partner lane l ^ 32
+// (swap32_pair), so that every lane stores 16 contiguous bytes, dims 32 db + 16 m + 8 kg .. + 7
+// (2 DB stores instead of 4 DB). With a gate, its 16-byte pieces for those dims are all loaded
+// first (each wait then covers only the pieces before it) and applied after the swap. The
+// caller keeps the whole wave in the call (the swaps read the partner lanes).
 template <int DB, bool GATE>
 __device__ __forceinline__ void store_block(const f32x16 (&o)[DB], float inv, int kg, __amdgpu_buffer_rsrc_t o_rs,
                                             int ooff, __amdgpu_buffer_rsrc_t g_rs, int goff) {
-    store_chunks<4 * DB, GATE>(
-        [&](int c) {
-            const int db = c >> 2, jj = c & 3;
-            return f32x4{o[db][4 * jj], o[db][4 * jj + 1], o[db][4 * jj + 2], o[db][4 * jj + 3]};
-        },
-        [&](int c) { return (c >> 2) * 32 + 8 * (c & 3) + 4 * kg; }, inv, o_rs, ooff, g_rs, goff);
+    constexpr int NP = 2 * DB;
+    auto dim0 = [&](int q) { return (q >> 1) * 32 + 16 * (q & 1) + 8 * kg; };
+    bf16x8 g[GATE ? NP : 1];
+    if constexpr (GATE) {
+#pragma unroll
+        for (int q = 0; q < NP; ++q) g[q] = buf_ld16_g(g_rs, goff + dim0(q) * 2);
+    }
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+        const int db = q >> 1, b = 8 * (q & 1);
+        const bf16x4 x = round4<false>(o[db][b] * inv, o[db][b + 1] * inv, o[db][b + 2] * inv, o[db][b + 3] * inv,
+                                       bf16x4{});
+        const bf16x4 y = round4<false>(o[db][b + 4] * inv, o[db][b + 5] * inv, o[db][b + 6] * inv,
+                                       o[db][b + 7] * inv, bf16x4{});
+        bf16x8 z = swap32_pair(x, y);
+        if constexpr (GATE) z = gate8(z, g[q]);
+        buf_st16(o_rs, ooff + dim0(q) * 2, z);
+    }
 }
 
 }  // namespace pe
