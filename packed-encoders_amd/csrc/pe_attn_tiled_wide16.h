@@ -35,12 +35,13 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Store two 4-dim bf16 chunks per lane of the 16x16 accumulator layout as 16 contiguous bytes:
-// x holds the lane's chunk of block 2j, y of block 2j + 1 (rows g4 = lane / 16 of 16 lanes).
-// v_permlane32_swap exchanges rows 2-3 of x with rows 0-1 of y, then v_permlane16_swap rows
-// 1 and 3 of x with rows 0 and 2 of y; row g4 then holds, in (x, y), the chunks of lanes
-// (2 (g4 % 2), 2 (g4 % 2) + 1) of block 2j + g4 / 2, and stores them at byte 16 g4.
-__device__ __forceinline__ void store16_pair(__amdgpu_buffer_rsrc_t r, int voff, bf16x4 x, bf16x4 y) {
+// Two 4-dim bf16 chunks per lane of the 16x16 accumulator layout regrouped into 8 contiguous
+// dims: x holds the lane's chunk of block 2j (dims 32 j + 4 g4 ..), y of block 2j + 1, rows
+// g4 = lane / 16 of 16 lanes. v_permlane32_swap exchanges rows 2-3 of x with rows 0-1 of y,
+// then v_permlane16_swap rows 1 and 3 of x with rows 0 and 2 of y; row g4 then holds, in
+// (x, y), the chunks of lanes (2 (g4 % 2), 2 (g4 % 2) + 1) of block 2j + g4 / 2: dims
+// 32 j + 8 g4 .. + 7, 16 contiguous bytes at byte 64 j + 16 g4 of the row.
+__device__ __forceinline__ bf16x8 swap16_pair(bf16x4 x, bf16x4 y) {
     typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
     u32x2 a = __builtin_bit_cast(u32x2, x), b = __builtin_bit_cast(u32x2, y);
 #pragma unroll
@@ -50,8 +51,15 @@ __device__ __forceinline__ void store16_pair(__amdgpu_buffer_rsrc_t r, int voff,
         a[k] = s16[0];
         b[k] = s16[1];
     }
-    const i32x4 v = {(int)a[0], (int)a[1], (int)b[0], (int)b[1]};
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, 0);
+    const bf16x4 lo = __builtin_bit_cast(bf16x4, a), hi = __builtin_bit_cast(bf16x4, b);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// bf16(x * s) of 8 outputs x already rounded to bf16 and 8 bf16 gate factors s.
+__device__ __forceinline__ bf16x8 scale8(bf16x8 x, bf16x8 s) {
+    const bf16x4 lo = round4<true>((float)x[0], (float)x[1], (float)x[2], (float)x[3], bf16x4{s[0], s[1], s[2], s[3]});
+    const bf16x4 hi = round4<true>((float)x[4], (float)x[5], (float)x[6], (float)x[7], bf16x4{s[4], s[5], s[6], s[7]});
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 // Run length of the XCD dealing for NW waves per workgroup and an NS-stage ring of 32 KB
@@ -197,29 +205,33 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
     reset();
 
     // Inputs of query tile qt held in registers: the Q fragment (lane (c16, g4): its row's dims
-    // 32 c + 8 g4 .. + 7) and, with a gate, bf16(sigmoid(gate)) of the dims it stores (16 db +
-    // 4 g4 + i). The loads are the compiler's (it places the wait before the first use); the
+    // 32 c + 8 g4 .. + 7) and, with a gate, bf16(sigmoid(gate)) of the dims it stores after the
+    // epilogue's regrouping (32 j + 8 g4 .. + 7, 16 bytes per load). The loads are the compiler's (it places the wait before the first use); the
     // empty asm makes that wait, and the sigmoids, happen here, outside the step loop: no step
     // waits on these loads, and the epilogue only scales, rounds and stores (the sigmoids run
     // while the CU's other workgroup is in its steps).
-    bf16x4 sgv[GATE ? DB : 1];
+    bf16x8 sgv[GATE ? DB / 2 : 1];  // gate factors of dims 32 j + 8 g4 .. + 7 (the epilogue's layout)
     auto load_tile_inputs = [&](int qt_) {
         const int row = qt_ * BM + rb * 16 + c16;
         const int base = row * q_row + 16 * g4;
 #pragma unroll
         for (int c = 0; c < DC; ++c) qf[c] = buf_ld16(q_rs, base + 64 * c, 0);
         if constexpr (GATE) {
-            const int gbase = row * (int)p.g_st * 2 + 8 * g4;
+            const int gbase = row * (int)p.g_st * 2 + 16 * g4;
 #pragma unroll
-            for (int db = 0; db < DB; ++db) sgv[db] = buf_ld8(g_rs, gbase + 32 * db, 0);
+            for (int j = 0; j < DB / 2; ++j) sgv[j] = buf_ld16(g_rs, gbase + 64 * j, 0);
         }
 #pragma unroll
         for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[c]));
         if constexpr (GATE) {
 #pragma unroll
-            for (int db = 0; db < DB; ++db) sgv[db] = sigmoid4(sgv[db]);
+            for (int j = 0; j < DB / 2; ++j) {
+                const bf16x4 lo = sigmoid4(bf16x4{sgv[j][0], sgv[j][1], sgv[j][2], sgv[j][3]});
+                const bf16x4 hi = sigmoid4(bf16x4{sgv[j][4], sgv[j][5], sgv[j][6], sgv[j][7]});
+                sgv[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
 #pragma unroll
-            for (int db = 0; db < DB; ++db) asm volatile("" : "+v"(sgv[db]));
+            for (int j = 0; j < DB / 2; ++j) asm volatile("" : "+v"(sgv[j]));
         }
     };
 
@@ -328,19 +340,20 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
             lt += __shfl_xor(lt, 32);
             if (wave_active) {
                 // Lane (c16, g4) rounds its 4-dim chunks (16 db + 4 g4 ..), then for each pair of
-                // 16-dim blocks (2j, 2j + 1) a 32-lane and a 16-lane swap regroup the four lanes
-                // of a row so that lane g4 holds dims 16 (2j + g4 / 2) + 8 (g4 % 2) .. + 7:
-                // 16 contiguous bytes at 64 j + 16 g4, one store per pair instead of two.
+                // 16-dim blocks (2j, 2j + 1) swap16_pair regroups the four lanes of a row so that
+                // lane g4 holds dims 32 j + 8 g4 .. + 7, whose gate factors it loaded: 16
+                // contiguous bytes at 64 j + 16 g4, one store per pair instead of two.
                 const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
                 const int ooff = myrow * (int)p.o_st * 2 + 16 * g4;
 #pragma unroll
                 for (int j = 0; j < DB / 2; ++j) {
-                    const bf16x4 y0 = round4<GATE>(o[2 * j][0] * inv, o[2 * j][1] * inv, o[2 * j][2] * inv,
-                                                   o[2 * j][3] * inv, sgv[GATE ? 2 * j : 0]);
-                    const bf16x4 y1 = round4<GATE>(o[2 * j + 1][0] * inv, o[2 * j + 1][1] * inv,
-                                                   o[2 * j + 1][2] * inv, o[2 * j + 1][3] * inv,
-                                                   sgv[GATE ? 2 * j + 1 : 0]);
-                    store16_pair(o_rs, ooff + 64 * j, y0, y1);
+                    const bf16x4 y0 = round4<false>(o[2 * j][0] * inv, o[2 * j][1] * inv, o[2 * j][2] * inv,
+                                                    o[2 * j][3] * inv, bf16x4{});
+                    const bf16x4 y1 = round4<false>(o[2 * j + 1][0] * inv, o[2 * j + 1][1] * inv,
+                                                    o[2 * j + 1][2] * inv, o[2 * j + 1][3] * inv, bf16x4{});
+                    bf16x8 z = swap16_pair(y0, y1);
+                    if constexpr (GATE) z = scale8(z, sgv[j]);
+                    buf_st16(o_rs, ooff + 64 * j, z);
                 }
             }
             reset();
