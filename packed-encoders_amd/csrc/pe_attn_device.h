@@ -81,7 +81,6 @@ __device__ __forceinline__ WorkItem load_work(const AttnParams &p, int entry) {
 }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 // Buffer resources. A raw buffer (stride 0) whose range ends at the last byte of a segment's
 // last row makes the hardware return 0 for any load beyond it and drop any store beyond it,
@@ -101,11 +100,8 @@ __device__ __forceinline__ uint32_t rows_bytes(int rows, int64_t stride, int d) 
 __device__ __forceinline__ bf16x8 buf_ld16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
-__device__ __forceinline__ bf16x4 buf_ld8(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
-}
-__device__ __forceinline__ void buf_st8(__amdgpu_buffer_rsrc_t r, int voff, bf16x4 x) {
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, x), r, voff, 0, 0);
+__device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t r, int voff, bf16x8 x) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), r, voff, 0, 0);
 }
 
 // Wave-uniform value as a scalar (lets the compiler branch on SCC instead of EXEC masks).
@@ -241,10 +237,6 @@ __device__ __forceinline__ bf16x4 round4(float a0, float a1, float a2, float a3,
     }
 }
 
-__device__ __forceinline__ bf16x8 buf_ld16_g(__amdgpu_buffer_rsrc_t r, int voff) { return buf_ld16(r, voff, 0); }
-__device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t r, int voff, bf16x8 x) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), r, voff, 0, 0);
-}
 
 // Two rounded 4-dim chunks of one query row, x held by lanes (col, kg) for dims d + 4 kg and y
 // for dims d + 8 + 4 kg, regrouped by one v_permlane32_swap per dword (x's lanes 32-63 with
@@ -287,7 +279,7 @@ __device__ __forceinline__ void store_block(const f32x16 (&o)[DB], float inv, in
     bf16x8 g[GATE ? NP : 1];
     if constexpr (GATE) {
 #pragma unroll
-        for (int q = 0; q < NP; ++q) g[q] = buf_ld16_g(g_rs, goff + dim0(q) * 2);
+        for (int q = 0; q < NP; ++q) g[q] = buf_ld16(g_rs, goff + dim0(q) * 2, 0);
     }
 #pragma unroll
     for (int q = 0; q < NP; ++q) {
