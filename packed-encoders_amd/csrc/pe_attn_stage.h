@@ -65,4 +65,43 @@ __device__ __forceinline__ bf16x4 tr16(const __bf16 *p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((PE_LDS lds_bf16x4 *)(PE_LDS void *)p);
 }
 
+// Epilogue of a wave's 32-row query block (32x32 accumulator layout, head_dim D) through its own
+// LDS region of 32 rows x D (row-major, 16-byte units XOR-swizzled per row): the scaled,
+// rounded rows go in as 16-byte units (swap32_pair gives each lane 8 contiguous dims) and
+// come back with lane l holding unit l % (D / 8) of row l / (D / 8), so every store writes
+// 64 / (D / 8) whole rows (whole 128-byte lines at D = 64) instead of 32 rows x 32 bytes. With
+// a gate, its 16-byte pieces of the same units are loaded first and applied on the way out.
+// The region must be idle (no other wave reading it, no load in flight into it); LDS accesses
+// of one wave complete in order, so the read-back sees the lane's own wave's writes.
+template <int D, bool GATE>
+__device__ __forceinline__ void store_rows(const f32x16 (&o)[D / 32], float inv, int lane, __bf16 *region,
+                                           __amdgpu_buffer_rsrc_t o_rs, int o_off0, int o_row,
+                                           __amdgpu_buffer_rsrc_t g_rs, int g_off0, int g_row) {
+    constexpr int DB = D / 32, CPR = D / 8, RPI = 64 / CPR, NR = 32 / RPI;
+    const int col = lane & 31, kg = lane >> 5;
+    const int urow = lane / CPR, unit = lane % CPR;
+    bf16x8 g[GATE ? NR : 1];
+    if constexpr (GATE) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) g[r] = buf_ld16(g_rs, g_off0 + (r * RPI + urow) * g_row + unit * 16, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 2 * DB; ++q) {
+        const int db = q >> 1, b = 8 * (q & 1);
+        const bf16x4 x = round4<false>(o[db][b] * inv, o[db][b + 1] * inv, o[db][b + 2] * inv, o[db][b + 3] * inv,
+                                       bf16x4{});
+        const bf16x4 y = round4<false>(o[db][b + 4] * inv, o[db][b + 5] * inv, o[db][b + 6] * inv,
+                                       o[db][b + 7] * inv, bf16x4{});
+        const int u = 4 * db + 2 * (q & 1) + kg;
+        *reinterpret_cast<bf16x8 *>(region + col * D + ((u ^ swz<CPR>(col)) * 8)) = swap32_pair(x, y);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int row = r * RPI + urow;
+        bf16x8 z = *reinterpret_cast<const bf16x8 *>(region + row * D + ((unit ^ swz<CPR>(row)) * 8));
+        if constexpr (GATE) z = gate8(z, g[r]);
+        buf_st16(o_rs, o_off0 + row * o_row + unit * 16, z);
+    }
+}
+
 }  // namespace pe
