@@ -173,9 +173,18 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
         }
         const float lt = ts + __shfl_xor(ts, 32);
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-        const int ooff = myrow * (int)p.o_st * 2;
-        const int goff = GATE ? myrow * (int)p.g_st * 2 : 0;
-        store_block<DB, GATE>(o, inv, kg, o_rs, ooff, g_rs, goff);
+        // With one head per wave (HPW 4) the head's K tile is read by this wave alone, so after
+        // the wave's last query block it is free for the row-wise epilogue (store_rows); LDS
+        // accesses of a wave complete in order, so no barrier is needed.
+        const bool last = i + 1 == NQ || (qb + WSTEP) * 32 >= L;
+        if (HPW == 4 && last) {
+            store_rows<D, GATE>(o, inv, lane, &kv[s][0][0], o_rs, r0 * (int)p.o_st * 2, (int)p.o_st * 2, g_rs,
+                                GATE ? r0 * (int)p.g_st * 2 : 0, GATE ? (int)p.g_st * 2 : 0);
+        } else {
+            const int ooff = myrow * (int)p.o_st * 2;
+            const int goff = GATE ? myrow * (int)p.g_st * 2 : 0;
+            store_block<DB, GATE>(o, inv, kg, o_rs, ooff, g_rs, goff);
+        }
     }
 }
 
