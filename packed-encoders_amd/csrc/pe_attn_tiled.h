@@ -416,16 +416,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
         }
 
         // Normalise, apply the gate, store. After the strip's last step the ring is idle (its
-        // loader stages nothing past the strip), so once every wave is past a barrier the last
-        // tile's rows leave through the ring's first stage as whole rows (store_rows).
+        // loader stages nothing past the strip), and the stage of the step before the last is
+        // free with no further barrier: every wave passed the last step's barrier, so is done
+        // with it, and no load was issued into it. The last tile's rows leave through that
+        // stage as whole rows (store_rows), each wave in its own 32-row region.
         const float lsum = (ls[0] + ls[1]) + (ls[2] + ls[3]);
         const float lt = lsum + __shfl_xor(lsum, 32);
         const bool via_lds = qt + 1 == qt_end;
-        if (via_lds) __syncthreads();
         if (wave_active) {
             const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
             if (via_lds) {
-                store_rows<D, GATE>(o, inv, lane, &ring[0][0][0] + wave * 32 * D, o_rs, r0 * (int)p.o_st * 2,
+                // `stage` already points past the last step's stage; the one before that is free.
+                const int free_stage = stage == 0 ? NS - 2 : stage == 1 ? NS - 1 : stage - 2;
+                store_rows<D, GATE>(o, inv, lane, &ring[free_stage][0][0] + wave * 32 * D, o_rs, r0 * (int)p.o_st * 2,
                                     (int)p.o_st * 2, g_rs, GATE ? r0 * (int)p.g_st * 2 : 0, GATE ? (int)p.g_st * 2 : 0);
             } else {
                 const int ooff = myrow * (int)p.o_st * 2;
