@@ -186,14 +186,22 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
     for (int seg = tid; seg < n_seq; seg += blockDim.x) serial_segment(seg, false);
     for (int i = wave; i < nqueued; i += nwaves) wave_segment(queue[i], false);
     __syncthreads();
-    if (tid == 0) {
-        int run = 0;
-        for (int b = 63; b >= 0; --b) {
-            off[b] = run;
-            run += cnt[b];
+    // Bucket offsets, costliest bucket first: lane i of wave 0 holds bucket 63 - i, and an
+    // inclusive shuffle scan over the wave gives each its start (a serial walk over the 64
+    // buckets was a chain of 64 dependent LDS round trips).
+    if (wave == 0) {
+        const int c = cnt[63 - lane];
+        int incl = c;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int up = __shfl_up(incl, d);
+            if (lane >= d) incl += up;
         }
-        count[0] = min(run, cap);
-        count[1] = run;
+        off[63 - lane] = incl - c;
+        if (lane == 63) {
+            count[0] = min(incl, cap);
+            count[1] = incl;
+        }
     }
     __syncthreads();
     for (int seg = tid; seg < n_seq; seg += blockDim.x) serial_segment(seg, true);
