@@ -181,25 +181,38 @@ def test_softmax_stability_and_determinism(pe, logit_scale, short_max):
     assert torch.equal(first, second)
 
 
+LARGE_LOGIT_LONG = [700, 300, 129, 65, 40, 16]
+LARGE_LOGIT_CASES = {
+    # id: (lengths, head_dim, kv heads, window, causal, short_max, band_kernel)
+    "global": (LARGE_LOGIT_LONG, 64, 4, (-1, -1), False, 0, 0),
+    "global-short": (LARGE_LOGIT_LONG, 64, 4, (-1, -1), False, 128, 0),
+    "band64": (LARGE_LOGIT_LONG, 64, 4, (64, 64), False, 0, 0),
+    "band64-stream": (LARGE_LOGIT_LONG, 64, 4, (64, 64), False, 0, 1),
+    "causal": (LARGE_LOGIT_LONG, 64, 4, (-1, -1), True, 0, 0),
+    "d128": (LARGE_LOGIT_LONG, 128, 4, (-1, -1), False, 0, 0),
+    "d256-causal": (LARGE_LOGIT_LONG, 256, 2, (-1, -1), True, 0, 0),
+    # 520 segments of 1..64 tokens: the short kernel with four heads per workgroup (it keeps
+    # four while segments x head groups fill two workgroups per CU)
+    "short-4heads": ([1 + (7 * i) % 64 for i in range(520)], 64, 4, (-1, -1), False, 64, 0),
+}
+
+
 @pytest.mark.parametrize("logit_scale", [2.0, 4.0])
-@pytest.mark.parametrize("d,hkv,window,causal,short_max", [
-    (64, 4, (-1, -1), False, 0), (64, 4, (-1, -1), False, 128), (64, 4, (64, 64), False, 0),
-    (64, 4, (-1, -1), True, 0), (128, 4, (-1, -1), False, 0), (256, 2, (-1, -1), True, 0)],
-    ids=["global", "global-short", "band64", "causal", "d128", "d256-causal"])
-def test_large_logits_match_oracle(pe, logit_scale, d, hkv, window, causal, short_max):
+@pytest.mark.parametrize("case", list(LARGE_LOGIT_CASES))
+def test_large_logits_match_oracle(pe, logit_scale, case):
     """Q and K drawn at 2x and 4x N(0,1): logits of about 10 and 40 natural units, rows whose
     near-tied top scores magnify any rounding of the scores themselves. Every kernel scales
     the fp32 Q.K product, as the reference does (triton_packed_attention.py:114), which keeps
     them inside the parity bar; a query operand rounded to bf16 after multiplying by the scale
     does not: a build of the global kernel that did so failed the two global cases here with
     max-abs 0.029 (2x) and 0.114 (4x), while passing every N(0,1) test."""
-    lengths = [700, 300, 129, 65, 40, 16]
-    announce(f"large logits x{logit_scale} d={d} window={window} causal={causal} short_max={short_max}")
+    lengths, d, hkv, window, causal, short_max, band_kernel = LARGE_LOGIT_CASES[case]
+    announce(f"large logits x{logit_scale} {case}")
     q, k, v, cu, _ = _inputs(lengths, hq=4, hkv=hkv, d=d, seed=29, logit_scale=logit_scale)
     qd, kd, vd, cud = _dev(q, k, v, cu)
     with torch.inference_mode():
         got = pe.varlen_attention(qd, kd, vd, cud, max(lengths), softmax_scale=d ** -0.5, window=window,
-                                  causal=causal, short_max=short_max)
+                                  causal=causal, short_max=short_max, band_kernel=band_kernel)
     want = _oracle(q, k, v, cu, scale=d ** -0.5, window=window, causal=causal)
     _assert_parity(got, want, cu)
 
