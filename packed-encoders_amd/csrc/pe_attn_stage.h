@@ -13,11 +13,32 @@ namespace pe {
 // A buffer offset past every resource's range: the load returns zeros and touches no memory.
 constexpr int kVoidOffset = 0x7ffffff0;
 
-// 16-byte unit of a row after the XOR swizzle: rows of CPR units; ds_read_b128 serves 16 lanes
-// (16 keys, one unit column) per pass over 64 banks, which this makes conflict-free.
+// 16-byte unit of a row after the XOR swizzle, rows of CPR units, over 64 LDS banks of 4 bytes.
+// Two reads must be conflict-free:
+//  * ds_read_b128 of a K (or Q) operand serves 16 lanes per pass: 16 consecutive keys, one
+//    unit column. The swizzle must be a bijection over the keys that share a bank row (the 8
+//    same-parity keys of a 16-key group at head_dim 64, where two 128-byte rows fill the 64
+//    banks; all 16 keys at head_dim 128).
+//  * ds_read_b64_tr_b16 of a V^T operand reads 8 consecutive keys (aligned to 8) x 4 units of
+//    one 32-dim block, 8 bytes per lane (512 bytes: two passes). The units after the XOR must
+//    cover the row's bank span evenly: at head_dim 64 two of each parity's four keys land in
+//    units 0-3 and two in units 4-7; at head_dim 128 each 4-unit block is hit by two keys.
+// Head_dim 64: j = bits 1-3 of the key, then bit 0 of j folded into bit 2 (0 5 2 7 4 1 6 3).
+// Head_dim 128: the key's low four bits with their two 2-bit halves exchanged. (A plain
+// (key >> 1) & 7 or key & 15 serves ds_read_b128 alike but leaves half of the banks idle in
+// every transposing read: four cycles instead of two.) Both depend only on key bits 0-3, so
+// offsets of whole 16-key halves and 32-key blocks never change a key's swizzle. Head_dim 256
+// rows span 8 bank rows and keep key & 15 (conflict-free for its 16x16 reads).
 template <int CPR>
 __device__ __forceinline__ int swz(int key) {
-    return CPR == 8 ? (key >> 1) & 7 : key & 15;
+    if constexpr (CPR == 8) {
+        const int j = (key >> 1) & 7;
+        return j ^ ((j & 1) << 2);
+    } else if constexpr (CPR == 16) {
+        return ((key & 3) << 2) | ((key >> 2) & 3);
+    } else {
+        return key & 15;
+    }
 }
 
 // Global -> LDS, 16 bytes per lane, four loads: load i's lane l data lands at lds[i] + 16 * l;
