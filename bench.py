@@ -34,6 +34,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import itertools
 import json
 import math
 import os
@@ -233,18 +234,21 @@ def gpu_bench(args, workload):
     torch.cuda.synchronize()
     pool = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in range(args.steps * len(timed_layers))]
-    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # an event at every step boundary: per-step GPU times for the samples' median and spread
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    g0.record(stream)
-    for _ in range(args.steps):
+    marks[0].record(stream)
+    for i in range(args.steps):
         step(pool)
-    g1.record(stream)
+        marks[i + 1].record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     wall_ms = (t1 - t0) * 1e3 / args.steps
-    gpu_ms = g0.elapsed_time(g1) / args.steps
-    kernel_ms = statistics.mean(a.elapsed_time(b) for a, b in timed)
+    gpu_ms = marks[0].elapsed_time(marks[-1]) / args.steps
+    per_step = [a.elapsed_time(b) for a, b in zip(marks, marks[1:])]
+    kernel_times = [a.elapsed_time(b) for a, b in timed]
+    kernel_ms = statistics.mean(kernel_times)
 
     # The same step captured once into a HIP graph and replayed: the launch cost a serving loop
     # that captures its packed forward pays (no host work per kernel).
@@ -291,13 +295,35 @@ def gpu_bench(args, workload):
     replay = None if graph_ms is None else {
         "ms_per_step": round(graph_ms, 4), "value": round(flops / (graph_ms * 1e-3) / 1e12, 3),
         "tokens_per_s": round(workload.total_tokens / (graph_ms * 1e-3), 1)}
+    roofline["kernel_ms_median"] = round(statistics.median(kernel_times), 4)
+    measured = achieved_peaks()
+    if measured is not None:  # this card's sustained rate (profiles/peaks.md), beside the spec peak
+        # the highest sustained rate of its kind (random-data MFMA; the faster of read and copy)
+        top = (measured["bf16_mfma_tflops_random"] if bound == "mfma"
+               else max(measured["hbm_read_gbs"], measured["hbm_copy_gbs_read_plus_write"]))
+        roofline["achieved_peak"] = top
+        roofline["frac_of_achieved_peak"] = round(achieved / top, 4)
     return {
-        "value": value, "ms_per_step": wall_ms, "gpu_ms_per_step": gpu_ms, "flops_per_step": flops,
+        "samples": step_samples(per_step, args.samples), "value": value, "ms_per_step": wall_ms,
+        "gpu_ms_per_step": gpu_ms, "flops_per_step": flops,
         "graph_replay": replay, "settle_s": round(settle_s, 3),
         "tokens_per_s": workload.total_tokens / (wall_ms * 1e-3), "roofline": roofline, "short_max": short_max,
         "min_seqlen": int(calls[0].args.min_seqlen),
         "_outputs": (calls, cu),
     }
+
+
+def step_samples(per_step: list[float], n: int) -> dict:
+    """The timed steps' GPU times (HIP events at every step boundary) cut into ``n`` consecutive
+    samples of equal step counts: each sample's mean ms per step, their median and their spread
+    ((max - min) / median), as the reference's dispatch benchmark reports medians of repeated
+    samples (benchmarks/packed_attention_dispatch_bench.py:169-229)."""
+    n = max(1, min(n, len(per_step)))
+    size = len(per_step) // n
+    means = [statistics.mean(per_step[i * size:(i + 1) * size]) for i in range(n)]
+    med = statistics.median(means)
+    return {"n": n, "steps_each": size, "ms_per_step": [round(m, 4) for m in means],
+            "median_ms_per_step": round(med, 4), "spread": round((max(means) - min(means)) / med, 4)}
 
 
 def sanity_check(calls, workload, cu):
@@ -523,7 +549,18 @@ def copy_calibration(steps: int) -> int:
     return 0
 
 
-PROFILED = ("C1", "Q4096", "C2", "C3", "C4", "C4-band", "C5")
+def _workload(name: str):
+    def make():
+        from packed_encoders_amd import workloads as w
+
+        return {"C1": w.c1, "C2": w.c2, "C3": w.c3, "C3-shuffled": lambda: w.c3(shuffled=True), "C4": w.c4,
+                "C4-band": lambda: w.c4(band=True), "C5": w.c5, "Q4096": w.query_sweep}[name]()
+
+    return make
+
+
+WORKLOADS = {name: _workload(name) for name in ("C1", "C2", "C3", "C3-shuffled", "C4", "C4-band", "C5", "Q4096")}
+PROFILED = ("C1", "Q4096", "C2", "C3", "C3-shuffled", "C4", "C4-band", "C5")
 SQ_PASSES = {  # two counter passes of at most 8 SQ counters (plus GRBM) each
     "SQA": "SQ_WAVES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_INSTS_SALU "
            "SQ_WAIT_INST_ANY GRBM_GUI_ACTIVE",
@@ -531,6 +568,7 @@ SQ_PASSES = {  # two counter passes of at most 8 SQ counters (plus GRBM) each
            "SQ_WAIT_INST_LDS SQ_LDS_BANK_CONFLICT SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE",
 }
 MFMA_PROFILED = ("C2", "C3", "C4", "C4-band", "C5")  # SQ counter passes (MFMA and VALU use, waits)
+KERNEL_PROFILED = ("C3-shuffled",)  # kernel trace only
 
 
 def profile_commands(out: str = "gpurun_out/prof") -> list[tuple[str, str]]:
@@ -544,6 +582,8 @@ def profile_commands(out: str = "gpurun_out/prof") -> list[tuple[str, str]]:
         run = f"python3 bench.py --workload {w} --no-cpu-baseline --no-model"
         cmds.append((f"{w}_kt", f"rocprofv3 --kernel-trace --stats --output-format csv -d {out}/{w}_kt -o k -- "
                                 f"{run} --steps 10 --warmup 2"))
+        if w in KERNEL_PROFILED:
+            continue
         run += " --no-graph --settle 0.05"  # counter passes: eager launches, short settle
         for pmc in ("FETCH_SIZE", "WRITE_SIZE"):
             cmds.append((f"{w}_{pmc}", f"rocprofv3 --pmc {pmc} --output-format csv -d {out}/{w}_{pmc} -o p -- "
@@ -596,9 +636,7 @@ def summarize_profiles(src: Path) -> int:
         table = _counters(src / f"copy_{pmc}" / "p_counter_collection.csv")
         per_copy = max(max(v[pmc]) for v in table.values() if pmc in v)  # the 1 GiB copies
         scale[pmc] = copy_bytes / (per_copy * 1024)
-    workloads = {"C1": pe.workloads.c1, "C2": pe.workloads.c2, "C3": pe.workloads.c3, "C4": pe.workloads.c4,
-                 "C4-band": lambda: pe.workloads.c4(band=True), "C5": pe.workloads.c5,
-                 "Q4096": pe.workloads.query_sweep}
+    workloads = WORKLOADS
     traffic = {"source_digest": digest,
                "calibration": {"copy_bytes": copy_bytes, "fetch_scale": round(scale["FETCH_SIZE"], 4),
                                "write_scale": round(scale["WRITE_SIZE"], 4)},
@@ -714,6 +752,153 @@ def summarize_profiles(src: Path) -> int:
     return 0
 
 
+def peaks(repeats: int = 7) -> int:
+    """Achieved peaks of this card (libpe_peaks.so, include/pe_peaks.h), beside the spec peaks
+    the roofline fractions divide by: bf16 MFMA (v_mfma_f32_32x32x16_bf16, four independent
+    chains per wave, eight waves per SIMD) on random and on all-zero operands (the chip's clock
+    under MFMA load depends on the bits it toggles), a streaming HBM read and an HBM copy with
+    16-byte vector loads, and the direct global-to-LDS loads the attention kernels stage with.
+    Each figure is the median of ``repeats`` HIP-event-timed launches after one warm-up. Prints
+    one JSON line; the committed summary is profiles/peaks.md (read by the bench line)."""
+    import torch
+
+    from packed_encoders_amd import _build
+
+    lib = ctypes.CDLL(str(_build.PEAKS_LIBRARY))
+    vp, i32, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
+    lib.pe_peak_mfma_bf16.argtypes = [vp, vp, i32, i32, vp]
+    lib.pe_peak_read.argtypes = [vp, sz, vp, i32, vp]
+    lib.pe_peak_copy.argtypes = [vp, vp, sz, i32, vp]
+    lib.pe_peak_read_lds.argtypes = [vp, sz, vp, i32, vp]
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    blocks = 256 * 8  # eight 4-wave workgroups per CU
+    sink = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+
+    def timed(launch) -> float:
+        launch()
+        times = []
+        for _ in range(repeats):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            launch()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e-3)
+        return statistics.median(times)
+
+    res = {"spec": {"bf16_mfma_tflops": PEAK_BF16_TFLOPS, "hbm_gbs": PEAK_HBM_GBS}, "repeats": repeats}
+    iters = 20000
+    flops = blocks * 16 * iters * 32768
+    g = torch.Generator(device=dev).manual_seed(5)
+    for name, ops in (("random", torch.randn(8 * 4096, device=dev, generator=g, dtype=torch.bfloat16)),
+                      ("zeros", torch.zeros(8 * 4096, device=dev, dtype=torch.bfloat16))):
+        t = timed(lambda: lib.pe_peak_mfma_bf16(ops.data_ptr(), sink.data_ptr(), blocks, iters, sp))
+        res[f"bf16_mfma_tflops_{name}"] = round(flops / t / 1e12, 1)
+    n = 4 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).random_(generator=g)
+    t = timed(lambda: lib.pe_peak_read(src.data_ptr(), n, sink.data_ptr(), blocks, sp))
+    res["hbm_read_gbs"] = round(n / t / 1e9, 1)
+    t = timed(lambda: lib.pe_peak_read_lds(src.data_ptr(), n, sink.data_ptr(), blocks, sp))
+    res["hbm_read_to_lds_gbs"] = round(n / t / 1e9, 1)
+    half = n // 2
+    t = timed(lambda: lib.pe_peak_copy(src.data_ptr(), src.data_ptr() + half, half, blocks, sp))
+    res["hbm_copy_gbs_read_plus_write"] = round(2 * half / t / 1e9, 1)
+    res["fraction_of_spec"] = {
+        "bf16_mfma_random": round(res["bf16_mfma_tflops_random"] / PEAK_BF16_TFLOPS, 3),
+        "bf16_mfma_zeros": round(res["bf16_mfma_tflops_zeros"] / PEAK_BF16_TFLOPS, 3),
+        "hbm_read": round(res["hbm_read_gbs"] / PEAK_HBM_GBS, 3),
+        "hbm_read_to_lds": round(res["hbm_read_to_lds_gbs"] / PEAK_HBM_GBS, 3),
+        "hbm_copy": round(res["hbm_copy_gbs_read_plus_write"] / PEAK_HBM_GBS, 3)}
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def achieved_peaks():
+    """The achieved peaks committed in profiles/peaks.md (its JSON line), or None."""
+    path = ROOT / "profiles" / "peaks.md"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("{") and "bf16_mfma_tflops_random" in line:
+                return json.loads(line)
+    except (OSError, ValueError):
+        return None
+    return None
+
+
+def band_sweep(reps: int = 10, replays: int = 5) -> int:
+    """The streaming band kernel against the tiled kernel on +-64 calls of every size: the
+    measurement the library's size rule (band kernel from a number of query tiles on, strip 8
+    from a larger one) is fitted to (attention_dispatch.fit_band_rule). Batches: C2-like
+    document mixes (LogNormal(400, 0.8) in [32, 2048]) of 16 to 1,024 documents and
+    equal-length batches of 256 to 8,192 tokens, 12 heads x 64. Per batch the tile plan is built
+    once and ``reps`` calls of the long-segment stage are graph-captured and replayed, cycling
+    over enough distinct Q/K/V sets that they do not stay resident in the 256 MB Infinity Cache
+    (a packed forward's layers each bring their own). Times: tiled kernel, band kernel at strips
+    4 and 8. One JSON line per batch; the committed summary is profiles/band_sweep.md
+    (the reference's counterpart: benchmarks/packed_attention_dispatch_bench.py:153-229)."""
+    import torch
+
+    from packed_encoders_amd import _lib, hip_attention as hip, workloads as W
+
+    lib = _lib.library()
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(13)
+    stream = torch.cuda.Stream(dev)
+    h, d = 12, 64
+    batches = []
+    for n_docs in (16, 32, 64, 128, 256, 512, 1024):
+        rng = W.SplitMix64(100 + n_docs)
+        batches.append((f"mix{n_docs}", tuple(rng.lognormal_length(400, 0.8, 32, 2048) for _ in range(n_docs))))
+    for L, n in ((256, 256), (512, 128), (512, 512), (1024, 64), (1024, 256), (2048, 32), (2048, 128),
+                 (4096, 32), (8192, 16), (8192, 32)):
+        batches.append((f"eq{L}x{n}", (L,) * n))
+    for name, lengths in batches:
+        T = sum(lengths)
+        per_set = 2 * T * h * d * 4  # q, k, v read and o written
+        n_sets = max(2, min(16, -(-600_000_000 // per_set)))
+        cu = torch.tensor([0, *itertools.accumulate(lengths)], dtype=torch.int32, device=dev)
+        sets = [tuple(torch.randn(T, h, d, device=dev, generator=gen, dtype=torch.bfloat16) for _ in range(3))
+                for _ in range(n_sets)]
+        outs = [torch.empty_like(s_[0]) for s_ in sets]
+        times = {}
+        for kind, band_kernel, strip in (("tiled", 2, 0), ("band4", 1, 4), ("band8", 1, 8)):
+            argss = [hip._args(q, k, v, o, cu, max(lengths), 0.125, 64, 64, False, None, 0, strip,
+                               band_kernel=band_kernel, min_seqlen=min(lengths)) for (q, k, v), o in zip(sets, outs)]
+            size = ctypes.c_size_t()
+            assert lib.pe_attn_workspace_size(ctypes.byref(argss[0]), ctypes.byref(size)) == 0
+            ws = torch.empty(max(size.value, 1), dtype=torch.uint8, device=dev)
+            with torch.cuda.stream(stream):
+                assert lib.pe_attn_plan(ctypes.byref(argss[0]), ws.data_ptr(), size.value, stream.cuda_stream) == 0
+                for a in argss:
+                    assert lib.pe_attn_tiled_fwd(ctypes.byref(a), ws.data_ptr(), size.value, stream.cuda_stream) == 0
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(reps):
+                    a = argss[i % n_sets]
+                    assert lib.pe_attn_tiled_fwd(ctypes.byref(a), ws.data_ptr(), size.value,
+                                                 torch.cuda.current_stream(dev).cuda_stream) == 0
+            graph.replay()
+            torch.cuda.synchronize()
+            samples = []
+            for _ in range(replays):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                graph.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                samples.append(e0.elapsed_time(e1) * 1e3 / reps)
+            times[kind] = statistics.median(samples)
+            del graph
+        print(json.dumps({"batch": name, "n_seq": len(lengths), "tokens": T, "query_tiles": T // 128 * h,
+                          "tiled_us": round(times["tiled"], 2), "band4_us": round(times["band4"], 2),
+                          "band8_us": round(times["band8"], 2)}), flush=True)
+        del sets, outs
+    return 0
+
+
 def dispatch_sweep(reps: int = 20, replays: int = 5) -> int:
     """Short kernel vs tiled kernel per segment length: the measurement the gfx950 routing
     boundary (attention_dispatch.HipDispatchPolicy) is fitted to. For head_dim 64 (12 heads)
@@ -782,7 +967,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="C2", help="C1 C2 C3 C4 C4-band C5 Q4096 (default C2)")
+    ap.add_argument("--workload", default="C2", help="C1 C2 C3 C3-shuffled C4 C4-band C5 Q4096 (default C2)")
+    ap.add_argument("--samples", type=int, default=5,
+                    help="consecutive samples the timed steps are cut into for the median and spread (default 5)")
     ap.add_argument("--short-max", type=int, default=None, help="routing boundary (default: gfx950 policy)")
     ap.add_argument("--strip", type=int, default=0, help="query tiles per tiled-kernel workgroup (0: library default)")
     ap.add_argument("--no-min-seqlen", action="store_true",
@@ -795,6 +982,10 @@ def main() -> int:
                     help="skip the end-to-end packed ModernBERT forward (C2 only)")
     ap.add_argument("--dispatch-sweep", action="store_true",
                     help="only time the short kernel against the tiled kernel per segment length")
+    ap.add_argument("--band-sweep", action="store_true",
+                    help="only time the streaming band kernel against the tiled kernel on +-64 calls of every size")
+    ap.add_argument("--peaks", action="store_true",
+                    help="only measure this card's achieved bf16 MFMA, HBM read/copy and global-to-LDS rates")
     ap.add_argument("--profile-commands", action="store_true",
                     help="only print the rocprofv3 commands behind the committed profiles (name<TAB>command)")
     ap.add_argument("--summarize-profiles", metavar="DIR",
@@ -817,13 +1008,15 @@ def main() -> int:
         return copy_calibration(args.steps)
     if args.dispatch_sweep:
         return dispatch_sweep()
+    if args.band_sweep:
+        return band_sweep()
+    if args.peaks:
+        return peaks()
 
     import packed_encoders_amd as pe
 
     w = args.workload
-    workload = {"C1": pe.workloads.c1, "C2": pe.workloads.c2, "C3": pe.workloads.c3, "C4": pe.workloads.c4,
-                "C4-band": lambda: pe.workloads.c4(band=True), "C5": pe.workloads.c5,
-                "Q4096": pe.workloads.query_sweep}[w]()
+    workload = WORKLOADS[w]()
     res = gpu_bench(args, workload)
     model_res = None
     if w == "C2" and not args.no_model:
@@ -870,6 +1063,7 @@ def main() -> int:
         },
         "tokens_per_s": round(res["tokens_per_s"], 1),
         "gpu_ms_per_step": round(res["gpu_ms_per_step"], 4),
+        "samples": res["samples"],
         "graph_replay": res["graph_replay"],
         "settle_s": res["settle_s"],
         "roofline": res["roofline"],

@@ -17,6 +17,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 INCLUDE = HERE.parent / "include"
 LIBRARY = HERE / "libpe_attn.so"
+PEAKS_LIBRARY = HERE / "libpe_peaks.so"  # achieved-peak microbenchmarks (include/pe_peaks.h)
 ARCH = "gfx950"
 
 # hipcc flags. Packed FP32 instructions are disabled for device code; hipcc's host pass warns
@@ -34,6 +35,7 @@ HIPCC_FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 SOURCES = ["pe_attn_capi.hip"]
+PEAKS_SOURCES = ["pe_peaks.hip"]
 
 
 def _code_only(text: str) -> str:
@@ -45,11 +47,12 @@ def _code_only(text: str) -> str:
 
 
 def source_digest() -> str:
-    """A short sha256 over the code of the library's HIP sources and public headers (comments
-    and layout excluded) and the compile flags: what ties a committed profile of the kernels to
-    the code it measured."""
+    """A short sha256 over the code of the attention library's HIP sources and public header
+    (comments and layout excluded; the peaks microbenchmarks are not part of it) and the
+    compile flags: what ties a committed profile of the kernels to the code it measured."""
     h = hashlib.sha256(" ".join(HIPCC_FLAGS).encode())
-    for path in sorted(p for p in [*CSRC.iterdir(), *INCLUDE.iterdir()] if p.is_file()):
+    files = [p for p in [*CSRC.iterdir(), *INCLUDE.iterdir()] if p.is_file() and "peaks" not in p.name]
+    for path in sorted(files):
         h.update(path.name.encode())
         h.update(_code_only(path.read_text()).encode())
     return h.hexdigest()[:16]
@@ -63,9 +66,16 @@ def hipcc() -> str:
 
 
 def build_library(verbose: bool = False) -> Path:
-    """Compile every HIP source into ``libpe_attn.so`` (atomic replace)."""
-    tmp = LIBRARY.with_name(f"{LIBRARY.name}.tmp{os.getpid()}")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", *(str(CSRC / s) for s in SOURCES), "-o", str(tmp)]
+    """Compile the attention library ``libpe_attn.so`` and the peaks microbenchmarks
+    ``libpe_peaks.so`` (each an atomic replace); returns the attention library's path."""
+    _compile(SOURCES, LIBRARY, verbose)
+    _compile(PEAKS_SOURCES, PEAKS_LIBRARY, verbose)
+    return LIBRARY
+
+
+def _compile(sources: list[str], target: Path, verbose: bool) -> None:
+    tmp = target.with_name(f"{target.name}.tmp{os.getpid()}")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", *(str(CSRC / s) for s in sources), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "packed-fp32-ops' is not a recognized feature"
     stderr = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
@@ -74,8 +84,7 @@ def build_library(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{' '.join(cmd)}\n{stderr}")
     if verbose and stderr.strip():
         print(stderr)
-    os.replace(tmp, LIBRARY)
-    return LIBRARY
+    os.replace(tmp, target)
 
 
 if __name__ == "__main__":

@@ -94,91 +94,110 @@ def packed_workload(*, total_tokens: int, n_sequences: int, max_seqlen: int) -> 
 # ----------------------------------------------------------------------------- layers
 
 
-def _layer_is_global(layer: nn.Module, layer_idx: int, params: ModernBertParams) -> bool:
-    kind = getattr(layer, "attention_type", None)
-    if kind == "full_attention":
-        return True
-    if kind == "sliding_attention":
-        return False
-    return params.is_global_layer(layer_idx)
+@dataclass(frozen=True)
+class LayerKind:
+    """What a layer's attention sees: RoPE tables, the dense path's additive mask, and the
+    (left, right) window the varlen kernels take — (-1, -1) for global layers."""
+
+    cos: Tensor
+    sin: Tensor
+    mask: Tensor | None
+    window: tuple[int, int]
 
 
-def encoder_layer(x: Tensor, pending_residual: Tensor | None, layer: nn.Module, params: ModernBertParams,
-                  cos: Tensor, sin: Tensor, mask: Tensor | None, window: tuple[int, int], backend: str, execution,
-                  cu_seqlens: Tensor | None = None, max_seqlen: int | None = None) -> tuple[Tensor, Tensor]:
-    """One ModernBERT layer. The residual of the MLP is returned unapplied: the next layer's
-    attention norm (or the final norm) adds it in its add+LayerNorm (forward.py:164-234)."""
-    b, s = x.shape[:2]
+def layer_schedule(model: nn.Module, params: ModernBertParams) -> list[bool]:
+    """Per encoder layer, whether it attends globally: the layer's own ``attention_type`` when
+    Hugging Face set one, else the config's period of global layers (config.py)."""
+    kinds = {"full_attention": True, "sliding_attention": False}
+    return [kinds.get(getattr(layer, "attention_type", None), params.is_global_layer(i))
+            for i, layer in enumerate(model.layers)]
+
+
+def _qkv_projection(x: Tensor, residual: Tensor | None, layer: nn.Module, execution) -> tuple[Tensor, Tensor]:
+    """Fold the previous layer's unapplied MLP residual into ``x`` (inside the add+LayerNorm when
+    the layer has an attention norm) and project the normed stream to ``qkv``. Returns
+    ``(x, qkv)``; a layer with ``nn.Identity`` as its attention norm projects ``x`` as is."""
+    norm = layer.attn_norm
+    if isinstance(norm, nn.Identity):
+        x = x if residual is None else x + residual
+        return x, execution.dense_linear(x, layer.attn.Wqkv.weight)
+    if residual is None:
+        normed = execution.layer_norm(x, norm.weight, norm.eps)
+    else:
+        x, normed = execution.add_layer_norm(x, residual, norm.weight, norm.eps)
+    return x, execution.linear(normed, layer.attn.Wqkv.weight)
+
+
+def _attention_context(qkv: Tensor, kind: LayerKind, params: ModernBertParams, backend: str, execution,
+                       cu_seqlens: Tensor | None, max_seqlen: int | None) -> Tensor:
+    """RoPE and attention over ``qkv [B, S, 3*H*D]``; returns the context ``[B, S, H*D]``.
+    The HIP path rotates q and k straight out of ``qkv`` into contiguous ``[B, S, H, D]`` and
+    leaves v a strided view (token stride 3HD) that the kernels read in place; the dense path
+    splits and transposes to ``[B, H, S, D]``."""
+    b, s = qkv.shape[:2]
     h, d = params.num_attention_heads, params.head_dim
-    attn_norm = layer.attn_norm
-    if isinstance(attn_norm, nn.Identity):
-        if pending_residual is not None:
-            x = x + pending_residual
-        qkv = execution.dense_linear(x, layer.attn.Wqkv.weight)
-    else:
-        if pending_residual is None:
-            normed = execution.layer_norm(x, attn_norm.weight, attn_norm.eps)
-        else:
-            x, normed = execution.add_layer_norm(x, pending_residual, attn_norm.weight, attn_norm.eps)
-        qkv = execution.linear(normed, layer.attn.Wqkv.weight)
-
     if ops.use_bshd_rope(backend, h, d, cu_seqlens):
-        # q, k contiguous [B, S, H, D] straight from qkv; v a strided view of it (token stride 3HD)
-        q, k = execution.rope_qkv(qkv, h, d, cos, sin)
-        v = qkv.view(b, s, 3, h, d)[:, :, 2]
-        ctx = execution.attention_bshd(q, k, v, window=window, scaling=params.scaling, cu_seqlens=cu_seqlens,
-                                       max_seqlen=max_seqlen, backend=backend)
-        del q, k, v
-    else:
-        q, k, v = qkv.view(b, s, 3, h, d).unbind(dim=2)
-        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
-        q, k = execution.rope(q, k, cos, sin)
-        ctx = execution.attention(q, k, v, mask=mask, window=window, scaling=params.scaling, backend=backend,
-                                  cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
-    wo = execution.linear(ctx, layer.attn.Wo.weight)
-    x, normed = execution.add_layer_norm(x, wo, layer.mlp_norm.weight, layer.mlp_norm.eps)
-    proj = execution.linear(normed, layer.mlp.Wi.weight)
-    pending = execution.linear(execution.geglu(proj), layer.mlp.Wo.weight)
-    return x, pending
+        q, k = execution.rope_qkv(qkv, h, d, kind.cos, kind.sin)
+        v = qkv.view(b, s, 3, h, d).select(2, 2)
+        return execution.attention_bshd(q, k, v, window=kind.window, scaling=params.scaling,
+                                        cu_seqlens=cu_seqlens, max_seqlen=max_seqlen, backend=backend)
+    q, k, v = (t.transpose(1, 2) for t in qkv.view(b, s, 3, h, d).unbind(dim=2))
+    q, k = execution.rope(q, k, kind.cos, kind.sin)
+    return execution.attention(q, k, v, mask=kind.mask, window=kind.window, scaling=params.scaling,
+                               backend=backend, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
+
+
+def encoder_layer(x: Tensor, residual: Tensor | None, layer: nn.Module, params: ModernBertParams, kind: LayerKind,
+                  backend: str, execution, cu_seqlens: Tensor | None = None,
+                  max_seqlen: int | None = None) -> tuple[Tensor, Tensor]:
+    """One ModernBERT layer in Hugging Face's order (attention half, then GeGLU MLP half). The
+    MLP's output is returned unapplied as the next residual: the next layer's attention norm,
+    or the final norm, adds it inside its add+LayerNorm (forward.py:164-234)."""
+    x, qkv = _qkv_projection(x, residual, layer, execution)
+    ctx = _attention_context(qkv, kind, params, backend, execution, cu_seqlens, max_seqlen)
+    x, normed = execution.add_layer_norm(x, execution.linear(ctx, layer.attn.Wo.weight), layer.mlp_norm.weight,
+                                         layer.mlp_norm.eps)
+    hidden = execution.geglu(execution.linear(normed, layer.mlp.Wi.weight))
+    return x, execution.linear(hidden, layer.mlp.Wo.weight)
 
 
 def core(model: nn.Module, params: ModernBertParams, x: Tensor, cos_global: Tensor, sin_global: Tensor,
          cos_local: Tensor, sin_local: Tensor, full_mask: Tensor | None, sliding_mask: Tensor | None, *,
          execution=None, backend: str = "sdpa", cu_seqlens: Tensor | None = None,
-         max_seqlen: int | None = None) -> Tensor:
-    """The layer loop and the final norm: device work only, so it can be captured
-    (forward.py:237-288). Global layers take window ``(-1, -1)``, local ones the half window."""
+         max_seqlen: int | None = None, min_seqlen: int = 0) -> Tensor:
+    """The encoder layers and the final norm: device work only, so it can be captured
+    (forward.py:237-288). ``min_seqlen`` is the host's lower bound on the packed segment lengths
+    (0 unknown), shared by every layer's HIP attention call."""
     execution = _execution_for(model, execution)
     half = params.sliding_half_window
-    pending = None
-    scope = _plan_scope(backend, cu_seqlens)
-    with scope:
-        for idx, layer in enumerate(model.layers):
-            if _layer_is_global(layer, idx, params):
-                cos, sin, mask, window = cos_global, sin_global, full_mask, (-1, -1)
-            else:
-                cos, sin, mask, window = cos_local, sin_local, sliding_mask, (half, half)
-            x, pending = encoder_layer(x, pending, layer, params, cos, sin, mask, window, backend, execution,
-                                       cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
+    kinds = {True: LayerKind(cos_global, sin_global, full_mask, (-1, -1)),
+             False: LayerKind(cos_local, sin_local, sliding_mask, (half, half))}
+    residual = None
+    with _plan_scope(backend, cu_seqlens, min_seqlen):
+        for layer, is_global in zip(model.layers, layer_schedule(model, params)):
+            x, residual = encoder_layer(x, residual, layer, params, kinds[is_global], backend, execution,
+                                        cu_seqlens=cu_seqlens, max_seqlen=max_seqlen)
     final = model.final_norm
-    if pending is None:
+    if residual is None:
         return execution.layer_norm(x, final.weight, final.eps)
-    return execution.add_layer_norm(x, pending, final.weight, final.eps)[1]
+    return execution.add_layer_norm(x, residual, final.weight, final.eps)[1]
 
 
 class _NullScope:
     def __enter__(self):
-        return self
+        return None
 
     def __exit__(self, *exc):
         return False
 
 
-def _plan_scope(backend: str, cu_seqlens: Tensor | None):
+def _plan_scope(backend: str, cu_seqlens: Tensor | None, min_seqlen: int = 0):
+    """The layers of one packed forward share ``cu_seqlens``: under the HIP backend they share
+    the device-built tile plans and the host's length bound (``hip_attention.shared_plans``)."""
     if backend == "hip" and cu_seqlens is not None:
         from .hip_attention import shared_plans
 
-        return shared_plans()
+        return shared_plans(min_seqlen)
     return _NullScope()
 
 
@@ -277,13 +296,15 @@ def repad(x_packed: Tensor, indices: Tensor, b: int, s: int) -> Tensor:
 
 def packed_forward(model: nn.Module, params: ModernBertParams, packed_ids: Tensor, cu_seqlens: Tensor,
                    max_seqlen: int, position_ids: Tensor, *, execution=None, backend: str | None = None,
-                   _allow_graph: bool = True) -> Tensor:
+                   _allow_graph: bool = True, min_seqlen: int = 0) -> Tensor:
     """Encode an already-packed batch; returns ``[total, hidden]`` in input order.
 
     ``packed_ids [T]`` int64, ``cu_seqlens [N+1]`` int32 on the device, ``max_seqlen`` a host
     int bounding every length, ``position_ids [T]`` int64 positions within each sequence
-    (``arange`` per sequence, as ``unpad`` makes them). With an active packed graph runner (no
-    autograd, no autocast) the call replays a captured graph instead.
+    (``arange`` per sequence, as ``unpad`` makes them). ``min_seqlen`` is an optional host lower
+    bound on the lengths (0 unknown): with every segment longer than the short kernel's
+    boundary, no layer launches the short pass. With an active packed graph runner (no
+    autograd, no autocast) the call replays a captured graph instead (captured for any lengths).
     """
     state = getattr(model, ATTR, None)
     requested = backend if backend is not None else (state.attention_backend if state is not None else "hip")
@@ -300,11 +321,12 @@ def packed_forward(model: nn.Module, params: ModernBertParams, packed_ids: Tenso
     if resolved == "sdpa":
         return packed_sdpa_fallback(model, params, packed_ids, cu_seqlens, max_seqlen, position_ids,
                                     execution=execution)
-    return packed_core(model, params, x, cu_seqlens, max_seqlen, position_ids, execution=execution)
+    return packed_core(model, params, x, cu_seqlens, max_seqlen, position_ids, execution=execution,
+                       min_seqlen=min_seqlen)
 
 
 def packed_core(model: nn.Module, params: ModernBertParams, x: Tensor, cu_seqlens: Tensor, max_seqlen: int,
-                position_ids: Tensor, *, execution) -> Tensor:
+                position_ids: Tensor, *, execution, min_seqlen: int = 0) -> Tensor:
     """RoPE tables up to ``max_seqlen`` gathered per token, then ``core`` on ``[1, T, hidden]``
     with the HIP backend. Shared by the eager packed forward and the graph runner's capture."""
     device, dtype, d = x.device, x.dtype, params.head_dim
@@ -318,7 +340,8 @@ def packed_core(model: nn.Module, params: ModernBertParams, x: Tensor, cu_seqlen
         return t[0].index_select(0, position_ids)[None]
 
     out = core(model, params, x[None], gather(cos_g), gather(sin_g), gather(cos_l), gather(sin_l), None, None,
-               execution=execution, backend="hip", cu_seqlens=cu_seqlens, max_seqlen=int(max_seqlen))
+               execution=execution, backend="hip", cu_seqlens=cu_seqlens, max_seqlen=int(max_seqlen),
+               min_seqlen=min(int(min_seqlen), int(max_seqlen)))
     return out[0]
 
 
@@ -343,8 +366,15 @@ def varlen_forward(model: nn.Module, params: ModernBertParams, input_ids: Tensor
     (``attention_mask`` None: every token is real)."""
     b, s = input_ids.shape
     ids, indices, cu, max_seqlen, positions = unpad(input_ids, attention_mask)
+    # the shortest row when the host holds the mask (or there is none): no device read
+    if attention_mask is None:
+        shortest = s
+    elif attention_mask.device.type == "cpu":
+        shortest = int(attention_mask.sum(dim=1).min()) if b else 0
+    else:
+        shortest = 0
     out = packed_forward(model, params, ids, cu, max_seqlen, positions, backend=backend, execution=execution,
-                         _allow_graph=True)
+                         _allow_graph=True, min_seqlen=shortest)
     return repad(out, indices, b, s)
 
 

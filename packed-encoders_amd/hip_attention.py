@@ -100,19 +100,27 @@ def _check_tensors(q: Tensor, k: Tensor, v: Tensor, cu: Tensor, gate: Tensor | N
 
 # Tile plans shared within a scope (one packed forward): key -> (cu_seqlens, workspace, bytes).
 _PLANS: contextvars.ContextVar[dict | None] = contextvars.ContextVar("pe_hip_shared_plans", default=None)
+_FLOOR: contextvars.ContextVar[int] = contextvars.ContextVar("pe_hip_min_seqlen", default=0)
 
 
 @contextlib.contextmanager
-def shared_plans():
+def shared_plans(min_seqlen: int = 0):
     """Within this scope, varlen attention calls that share a ``cu_seqlens`` tensor, head
     geometry, window, causality and routing boundary build the tiled kernel's plan once and
     reuse it: a packed forward's 22 layers then run 2 plan kernels (global and local) instead
     of 22. The scope keeps each plan's workspace (and its ``cu_seqlens``) alive until it exits;
-    the caller must not change ``cu_seqlens`` values inside the scope."""
+    the caller must not change ``cu_seqlens`` values inside the scope.
+
+    ``min_seqlen`` is the host's lower bound on the shared batch's segment lengths (a collator
+    knows them; 0 when unknown). Calls in the scope that pass no ``min_seqlen`` of their own use
+    it, so a batch with no short segment skips the short kernel's launch in every layer. A
+    wrong bound changes which kernel serves a segment, never the result's correctness."""
     token = _PLANS.set({})
+    floor = _FLOOR.set(max(0, int(min_seqlen)))
     try:
         yield
     finally:
+        _FLOOR.reset(floor)
         _PLANS.reset(token)
 
 
@@ -292,14 +300,15 @@ def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_se
     kernel, 2 the tiled kernel; results agree within bf16 rounding, not bit for bit.
 
     ``min_seqlen`` is an optional host lower bound on the query segment lengths (a collator
-    that packs host-known lengths has it beside ``max_seqlen``). When it exceeds the routing
+    that packs host-known lengths has it beside ``max_seqlen``; None takes the enclosing
+    ``shared_plans`` scope's bound, 0 outside one). When it exceeds the routing
     boundary no segment can be short, and the call skips the short kernel's launch: every
     segment goes to the tiled kernels, which serve any length, so a wrong bound costs time,
     never results.
     """
     if band_kernel not in (0, 1, 2):
         raise ValueError("band_kernel must be 0 (library choice), 1 (streaming band) or 2 (tiled)")
-    min_seqlen = 0 if min_seqlen is None else int(min_seqlen)
+    min_seqlen = min(_FLOOR.get(), int(max_seqlen)) if min_seqlen is None else int(min_seqlen)
     if not 0 <= min_seqlen <= int(max_seqlen):
         raise ValueError(f"min_seqlen must lie in [0, max_seqlen], got {min_seqlen} (max_seqlen {max_seqlen})")
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):

@@ -141,13 +141,15 @@ def attention_bshd(q: Tensor, k: Tensor, v: Tensor, *, window: tuple[int, int], 
         raise ValueError(f"BSHD attention runs on the HIP kernels only (backend={backend!r})")
     varlen_attention = _load_hip_attention()
     b, s, h, d = q.shape
+    floor = None  # packed: the enclosing shared_plans scope's host bound
     if cu_seqlens is None:
         cu_seqlens = torch.arange(0, (b + 1) * s, s, dtype=torch.int32, device=q.device)
-        max_seqlen = s
+        max_seqlen = floor = s  # every row one segment of exactly s tokens
     elif b != 1:
         raise ValueError("packed attention takes a batch of one flat sequence")
     out = varlen_attention(q.reshape(b * s, h, d), k.reshape(b * s, k.shape[2], d), v.reshape(b * s, v.shape[2], d),
-                           cu_seqlens, int(max_seqlen), softmax_scale=scaling, window=tuple(window))
+                           cu_seqlens, int(max_seqlen), softmax_scale=scaling, window=tuple(window),
+                           min_seqlen=floor)
     return out.reshape(b, s, h * d)
 
 

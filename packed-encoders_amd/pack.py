@@ -163,8 +163,11 @@ class PackedModernBert:
             raise PackedEncodersError("packed metadata must be on the token device")
         if ids.numel() == 0 or batch.max_seqlen <= 0:
             raise PackedEncodersError("empty packed batches are unsupported")
+        # host lengths, when the collator gives them, bound the shortest segment (no device read)
+        shortest = min(batch.host_lengths, default=0) if batch.host_lengths else 0
         return forward.packed_forward(self.encoder, self.state.params, ids, cu, batch.max_seqlen, positions,
-                                      backend=self.state.attention_backend)
+                                      backend=self.state.attention_backend,
+                                      min_seqlen=max(0, min(int(shortest), int(batch.max_seqlen))))
 
     def set_cuda_graph(self, enabled: bool, config: GraphConfig | None = None) -> None:
         if enabled and self.state.packed_graph_runner is None:

@@ -152,7 +152,9 @@ def _hip(window, scale) -> tuple[Callable, ...]:
     varlen_attention = ops._load_hip_attention()  # ImportError when the library is unavailable
 
     def packed(q, k, v, cu32, max_len, lengths, causal):
-        return varlen_attention(q, k, v, cu32, max_len, softmax_scale=scale, window=window, causal=causal)
+        shortest = min((int(n) for n in lengths), default=0)  # host lengths: no short pass when none is short
+        return varlen_attention(q, k, v, cu32, max_len, softmax_scale=scale, window=window, causal=causal,
+                                min_seqlen=min(shortest, int(max_len)))
 
     def padded(q, k, v, static: PaddedStatic, causal):
         # [real | pad] segments: pads attend among themselves and their rows are discarded
@@ -161,8 +163,9 @@ def _hip(window, scale) -> tuple[Callable, ...]:
 
     def prefixed(q, k, v, cu_q, cu_k, max_q, max_k, lengths_q, lengths_k, causal):
         # query segment s is the tail of key segment s: the kernels' separate key segments
+        shortest = min((int(n) for n in lengths_q), default=0)
         return varlen_attention(q, k, v, cu_q, max_q, softmax_scale=scale, window=window, causal=causal,
-                                cu_seqlens_k=cu_k, max_seqlen_k=max_k)
+                                cu_seqlens_k=cu_k, max_seqlen_k=max_k, min_seqlen=min(shortest, int(max_q)))
 
     return packed, padded, prefixed
 

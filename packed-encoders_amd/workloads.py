@@ -9,7 +9,8 @@ Configurations (the workloads the benchmark baseline names):
   C2  ModernBERT-base: 64 docs, L = clip(round(LogNormal(ln 400, 0.8)), 32, 2048), 12 x 64,
       22 layers: every 3rd global, the rest a +-64 band
   C3  512 queries L ~ U{8..48} then 64 docs L = clip(round(LogNormal(ln 700, 0.8)), 256, 8192),
-      12 x 64, global (sigma 0.8 is an assumption: the configuration names none)
+      12 x 64, global (sigma 0.8 is an assumption: the configuration names none); C3-shuffled is
+      the same 576 segments in a seeded Fisher–Yates order (queries and documents interleaved)
   C4  16 x 8192, 16 heads x 64, global and +-64 band
   C5  256 segments, L ~ U{16..512}, 8 query / 2 kv heads x 256, causal, sigmoid gate
 """
@@ -125,8 +126,9 @@ def c3(seed: int = 3, shuffled: bool = False) -> Workload:
         for i in range(len(lengths) - 1, 0, -1):
             j = rng.randint(0, i)
             lengths[i], lengths[j] = lengths[j], lengths[i]
-    return Workload("C3", tuple(lengths), 12, 12, 64, (GLOBAL,),
-                    "512 queries U{8..48} + 64 docs LogNormal(700, 0.8) in [256, 8192], 12x64, global",
+    order = ", shuffled" if shuffled else ""
+    return Workload("C3-shuffled" if shuffled else "C3", tuple(lengths), 12, 12, 64, (GLOBAL,),
+                    f"512 queries U{{8..48}} + 64 docs LogNormal(700, 0.8) in [256, 8192]{order}, 12x64, global",
                     {"n_queries": 512})
 
 

@@ -1,12 +1,16 @@
 """GPU parity and invariants of the streaming band kernel (band64_attn_kernel), forced with
 ``band_kernel=1`` at sizes the library would otherwise give the tiled kernel.
 
-It serves head_dim 64 windows whose rows each span five 32-key blocks (ModernBERT's +-64 and
-any (left, right) in [33, 64] x [33, 64]), one query head per kv head group. Checked: the
-oracle on segment lengths straddling every block and tile edge, MHA and GQA 3:1, the fused
-gate, strips of 1..8 tiles bit-identical to each other, a stale running maximum past the
-overflow guard, zero cross-segment leakage and independence from batch composition (bit for
-bit), and agreement with the tiled kernel within the bf16 tolerance.
+It serves head_dim 64 windows whose rows each span five 32-key blocks, one query head per kv
+head group: left and right bounds whose block counts ceil(left / 32) + ceil(right / 32) sum to
+four — (33..64, 33..64) such as ModernBERT's +-64, (1..32, 65..96), (65..96, 1..32),
+(0, 97..128), (97..128, 0), and causal with a left window of 97..128 (causal is a right bound
+of 0). Checked: the oracle on segment lengths straddling every block and tile edge for the
+extreme shapes of every such class, MHA and GQA 3:1, the fused gate, strips of 1..8 tiles
+bit-identical to each other, a stale running maximum past the overflow guard, zero
+cross-segment leakage and independence from batch composition (bit for bit), agreement with
+the tiled kernel within the bf16 tolerance, and a segment whose kernel changes with the size
+of the call it is packed in (the library's size rule) within the same tolerance.
 """
 
 from __future__ import annotations
@@ -21,33 +25,39 @@ from test_hip_attention import WINDOW_LENGTHS, _assert_parity, _dev, _inputs, _o
 pytestmark = pytest.mark.gpu
 
 BAND_WINDOWS = [(64, 64), (33, 33), (40, 60), (64, 33)]
+# The extreme (left, right) of every block-count class the band kernel admits besides
+# (33..64, 33..64), and causal with a left window (window, causal).
+CLASS_EXTREMES = [((0, 97), False), ((0, 128), False), ((97, 0), False), ((128, 0), False),
+                  ((1, 65), False), ((1, 96), False), ((32, 65), False), ((32, 96), False),
+                  ((65, 1), False), ((65, 32), False), ((96, 1), False), ((96, 32), False),
+                  ((33, 64), False), ((97, -1), True), ((128, -1), True)]
 
 
-def _kernel_of(q, k, cu, max_seqlen, window, band_kernel):
+def _kernel_of(q, k, cu, max_seqlen, window, band_kernel, causal=False):
     import ctypes
 
     from packed_encoders_amd import _lib, hip_attention as hip
 
     out = torch.empty_like(q)
-    a = hip._args(q, k, k, out, cu, max_seqlen, 0.125, window[0], window[1], False, None, 0,
+    a = hip._args(q, k, k, out, cu, max_seqlen, 0.125, window[0], window[1], causal, None, 0,
                   band_kernel=band_kernel)
     res = (ctypes.c_int32 * 6)()
     assert _lib.library().pe_attn_kernels(ctypes.byref(a), res) == 0
     return res[1], res[2]
 
 
-def _run(pe, q, k, v, cu, mx, window, band_kernel=1, gate=None, strip=None):
+def _run(pe, q, k, v, cu, mx, window, band_kernel=1, gate=None, strip=None, causal=False):
     if strip is None:
         with torch.inference_mode():
             return pe.varlen_attention(q, k, v, cu, mx, softmax_scale=0.125, window=window, short_max=0,
-                                       gate=gate, band_kernel=band_kernel)
+                                       gate=gate, band_kernel=band_kernel, causal=causal)
     import ctypes
 
     from packed_encoders_amd import _lib, hip_attention as hip
 
     lib = _lib.library()
     out = torch.empty_like(q)
-    a = hip._args(q, k, v, out, cu, mx, 0.125, window[0], window[1], False, gate, 0, strip=strip,
+    a = hip._args(q, k, v, out, cu, mx, 0.125, window[0], window[1], causal, gate, 0, strip=strip,
                   band_kernel=band_kernel)
     size = ctypes.c_size_t()
     assert lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size)) == 0
@@ -74,6 +84,50 @@ def test_band_kernel_matches_oracle_and_strips_agree(pe, window, hq, hkv):
     _assert_parity(got, want, cu)
     for strip in (1, 2, 3, 8):
         assert torch.equal(_run(pe, qd, kd, vd, cud, mx, window, strip=strip), got), strip
+
+
+@pytest.mark.parametrize("window,causal", CLASS_EXTREMES,
+                         ids=[f"{w[0]}_{w[1]}{'c' if c else ''}" for w, c in CLASS_EXTREMES])
+def test_band_kernel_every_admitted_window_class(pe, window, causal):
+    """Every window shape the band kernel accepts, at the extremes of its block-count class,
+    forced onto the band kernel: the oracle, and strips of 1 and 3 tiles bit-identical."""
+    from packed_encoders_amd import _lib
+
+    announce(f"band kernel window class {window} causal={causal}")
+    q, k, v, cu, _ = _inputs(WINDOW_LENGTHS, hq=4, seed=67)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    mx = max(WINDOW_LENGTHS)
+    assert _kernel_of(qd, kd, cud, mx, window, 1, causal)[0] == _lib.KERNEL_BAND64
+    got = _run(pe, qd, kd, vd, cud, mx, window, causal=causal)
+    torch.cuda.synchronize()
+    want = _oracle(q, k, v, cu, scale=0.125, window=window, causal=causal)
+    _assert_parity(got, want, cu)
+    for strip in (1, 3):
+        assert torch.equal(_run(pe, qd, kd, vd, cud, mx, window, strip=strip, causal=causal), got), strip
+
+
+def test_segment_across_the_size_rule(pe):
+    """A +-64 segment alone (a small call: the tiled kernel) and the same segment packed into a
+    call of at least 6,144 query tiles (the band kernel) agree within the parity bar, not bit
+    for bit: the library's size rule is the one way a segment's bits depend on its batch."""
+    from packed_encoders_amd import _lib
+
+    announce("segment alone (tiled) vs in a large call (band)")
+    lengths = [1000] + [4096] * 16
+    q, k, v, cu, _ = _inputs(lengths, hq=12, seed=68)
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    mx = max(lengths)
+    assert _kernel_of(qd, kd, cud, mx, (64, 64), 0)[0] == _lib.KERNEL_BAND64
+    big = _run(pe, qd, kd, vd, cud, mx, (64, 64), band_kernel=0)
+    one = torch.tensor([0, 1000], dtype=torch.int32, device="cuda")
+    assert _kernel_of(qd[:1000], kd[:1000], one, 1000, (64, 64), 0)[0] == _lib.KERNEL_TILED
+    alone = _run(pe, qd[:1000].contiguous(), kd[:1000].contiguous(), vd[:1000].contiguous(), one, 1000, (64, 64),
+                 band_kernel=0)
+    torch.cuda.synchronize()
+    want = _oracle(q[:1000], k[:1000], v[:1000], cu[:2], scale=0.125, window=(64, 64))
+    _assert_parity(alone, want, cu[:2])
+    _assert_parity(big[:1000], want, cu[:2])
+    assert (alone.float() - big[:1000].float()).abs().max().item() <= 2e-2
 
 
 def test_band_kernel_gate_and_agreement_with_tiled(pe):

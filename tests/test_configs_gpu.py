@@ -7,7 +7,8 @@ every segment's first and last row, the rows on either side of every 32-row bloc
 128-row query-tile edge, and seeded random rows, at the north-star bar: max-abs <= 2e-2 and
 per-token cosine >= 0.9999 (the reference's harness checks outputs on the shapes it times,
 benchmarks/packed_short_attention_bench.py:96-117,243-309). Every output row must be finite.
-C3's rows cover both kernels of its mixed call (segments <= 64 tokens take the short kernel).
+C3's rows cover both kernels of its mixed call (segments <= 64 tokens take the short kernel), in
+its generated order (queries, then documents) and shuffled (the two interleaved).
 """
 
 from __future__ import annotations
@@ -55,13 +56,14 @@ def _workloads():
         "C2-global": (c2, 0),
         "C2-band": (c2, 1),
         "C3": (w.c3(), 0),
+        "C3-shuffled": (w.c3(shuffled=True), 0),
         "C4": (w.c4(), 0),
         "C4-band": (w.c4(band=True), 0),
         "C5": (w.c5(), 0),
     }
 
 
-@pytest.mark.parametrize("name", ["C1", "C2-global", "C2-band", "C3", "C4", "C4-band", "C5"])
+@pytest.mark.parametrize("name", ["C1", "C2-global", "C2-band", "C3", "C3-shuffled", "C4", "C4-band", "C5"])
 def test_benchmark_workload_matches_oracle(pe, name):
     workload, layer_index = _workloads()[name]
     layer = workload.layers[layer_index]

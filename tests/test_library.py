@@ -46,6 +46,21 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib, name)
 
 
+def test_peaks_library_exports_its_header():
+    """libpe_peaks.so (achieved-peak microbenchmarks) exports every entry point
+    include/pe_peaks.h declares."""
+    from packed_encoders_amd import _build
+
+    text = (ROOT / "include" / "pe_peaks.h").read_text()
+    declared = set(re.findall(r"^\s*int\s+(pe_peak_\w+)\s*\(", text, flags=re.M))
+    assert declared == {"pe_peak_mfma_bf16", "pe_peak_read", "pe_peak_copy", "pe_peak_read_lds"}
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_build.PEAKS_LIBRARY)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    assert declared <= exported
+    assert b"gfx950" in _build.PEAKS_LIBRARY.read_bytes()
+
+
 def test_library_holds_gfx950_code():
     from packed_encoders_amd import _build
 
@@ -282,6 +297,35 @@ def test_kernel_choice_per_call(lib):
     n_long = min(64, 32438 // 65)
     tiles = (32438 + n_long * 127) // 128
     assert rc == 0 and size == 256 + 16 * min(64 * 4, (tiles + n_long * 3) // 4)
+
+
+def test_band_kernel_envelope_is_the_tested_one(lib):
+    """Every (left, right, causal) the streaming band kernel accepts (band_kernel=1, host-only
+    kernel choice) lies in a block-count class whose extreme shapes the GPU tests force onto it
+    (tests/test_band_kernel_gpu.py: BAND_WINDOWS and CLASS_EXTREMES), inside those extremes."""
+    import math
+
+    from packed_encoders_amd import _lib
+
+    # block-count class (ceil(left / 32), ceil(right / 32)) -> tested (min, max) of left and right
+    tested = {(0, 4): ((0, 0), (97, 128)), (4, 0): ((97, 128), (0, 0)), (1, 3): ((1, 32), (65, 96)),
+              (3, 1): ((65, 96), (1, 32)), (2, 2): ((33, 64), (33, 64))}
+    admitted = 0
+    for causal in (0, 1):
+        for wl in range(-1, 200):
+            for wr in ([-1] if causal else range(-1, 200)):
+                out = (ctypes.c_int32 * 6)()
+                a = _args(band_kernel=1, window_left=wl, window_right=wr, causal=causal)
+                assert lib.pe_attn_kernels(ctypes.byref(a), out) == 0
+                if out[1] != _lib.KERNEL_BAND64:
+                    continue
+                admitted += 1
+                right = 0 if causal else wr
+                cls = (math.ceil(wl / 32), math.ceil(right / 32))
+                assert cls in tested, (wl, wr, causal)
+                (l0, l1), (r0, r1) = tested[cls]
+                assert l0 <= wl <= l1 and r0 <= right <= r1, (wl, wr, causal)
+    assert admitted == 32 + 32 + 32 * 32 * 2 + 32 * 32 + 32, admitted
 
 
 def test_min_seqlen_above_the_boundary_skips_the_short_pass(lib):

@@ -52,6 +52,7 @@ class Spy:
 
         real = _lib.library()
         self.calls = {}
+        self.short_launches = 0  # pe_attn_short_fwd calls that launch a kernel (pe_attn_kernels)
         spy = self
 
         class Proxy:
@@ -62,6 +63,12 @@ class Spy:
 
                 def wrapped(*args):
                     spy.calls[name] = spy.calls.get(name, 0) + 1
+                    if name == "pe_attn_short_fwd":
+                        import ctypes
+
+                        out = (ctypes.c_int32 * 6)()
+                        assert real.pe_attn_kernels(args[0], out) == 0
+                        spy.short_launches += out[0] > 0
                     return fn(*args)
 
                 return wrapped
@@ -192,6 +199,56 @@ def test_modernbert_base_shape_packed_forward(pe):
     cos = token_cosine(hip, dense)
     assert torch.isfinite(hip).all()
     assert cos.min() >= 0.99 and cos.mean() >= 0.999, (cos.min(), cos.mean())
+
+
+def test_c2_full_batch_forward_matches_hf_fp32(pe, monkeypatch):
+    """The headline workload end to end: ModernBERT-base (22 layers, hidden 768, 12 x 64, random
+    init) on C2's full batch of 64 documents through ``pe.pack`` with the collator's host
+    lengths, against Hugging Face's fp32 forward of the same weights (each document on its own,
+    no padding), per token. The bf16 dense SDPA path of this package on the same packed batch
+    is the control: the HIP path must be at least as close to fp32, up to a small margin. The
+    C-ABI spy checks the launches are the benchmark step's: two tile plans, one tiled call per
+    layer and no short pass (the shortest document, 98 tokens, is past the boundary of 64)."""
+    from transformers import ModernBertConfig, ModernBertModel
+
+    from packed_encoders_amd import forward, workloads
+
+    announce("C2 full batch, 22 layers, vs HF fp32")
+    wl = workloads.c2()
+    lengths = list(wl.lengths)
+    cfg = ModernBertConfig(vocab_size=50368, hidden_size=768, intermediate_size=1152, num_hidden_layers=22,
+                           num_attention_heads=12, local_attention=128, global_attn_every_n_layers=3,
+                           global_rope_theta=160000.0, local_rope_theta=10000.0, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    ref = ModernBertModel(cfg).eval().cuda()
+    model = copy.deepcopy(ref).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(77)
+    ids = torch.randint(0, cfg.vocab_size, (sum(lengths),), generator=g).cuda()
+    c = wl.cu_seqlens()
+    cu = torch.tensor(c, dtype=torch.int32, device="cuda")
+    positions = torch.cat([torch.arange(n, device="cuda") for n in lengths])
+    want = torch.empty(sum(lengths), cfg.hidden_size, device="cuda")
+    with torch.no_grad():
+        for a, b in zip(c, c[1:]):
+            want[a:b] = ref(input_ids=ids[a:b][None]).last_hidden_state[0]
+    del ref
+    pe.pack(model, attention_backend="hip", validate=False)
+    engine = pe.get_engine(model)
+    spy = Spy(monkeypatch)
+    with torch.no_grad(), pe.no_cuda_graph(model):
+        got = engine.forward_packed(pe.PackedBatch(ids, cu, max(lengths), positions, host_lengths=tuple(lengths)))
+    assert spy.calls.get("pe_attn_plan") == 2 and spy.calls.get("pe_attn_tiled_fwd") == 22
+    assert spy.short_launches == 0, spy.short_launches
+    params = pe.config.ModernBertParams.from_hf_config(cfg)
+    with torch.no_grad():
+        dense = forward.packed_sdpa_fallback(model, params, ids, cu, max(lengths), positions)
+    pe.unpack(model)
+    assert torch.isfinite(got).all()
+    cos, cos_dense = token_cosine(got, want), token_cosine(dense, want)
+    print(f"[c2 vs fp32] hip min {cos.min():.5f} mean {cos.mean():.6f}; "
+          f"bf16 sdpa min {cos_dense.min():.5f} mean {cos_dense.mean():.6f}", flush=True)
+    assert cos.mean() >= 0.999 and cos.min() >= 0.99, (cos.min(), cos.mean())
+    assert cos.mean() >= cos_dense.mean() - 2e-4 and cos.min() >= cos_dense.min() - 5e-3
 
 
 def test_padded_forward_with_a_host_mask_never_synchronises(pe):
