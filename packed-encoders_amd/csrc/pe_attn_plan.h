@@ -29,18 +29,51 @@ __device__ __forceinline__ int plan_tile_cost(int t, int bm, int L, int Lk, int 
     return max(1, khi - klo);
 }
 
+// Keys visited by query tiles [t0, t1) of a segment of nq tiles. Two shapes have a closed form:
+// global (every tile visits all Lk keys) and causal with no left window (tile t visits the keys
+// up to its last row, (t + 1) bm + off, the last tile up to Lk); others add tile by tile.
+__device__ __forceinline__ int64_t plan_tiles_cost(int t0, int t1, int nq, int bm, int L, int Lk, int wl, int wr) {
+    if (t1 <= t0) return 0;
+    if (wl < 0 && wr < 0) return (int64_t)(t1 - t0) * max(1, Lk);
+    const int off = Lk - L;
+    if (wl < 0 && wr == 0 && off >= 0) {
+        const int64_t a = t0, b = min(t1, nq - 1);  // full tiles [a, b): sum of (t + 1) bm + off
+        int64_t cost = b > a ? (int64_t)bm * (b * (b + 1) / 2 - a * (a + 1) / 2) + (b - a) * off : 0;
+        if (t1 >= nq) cost += Lk;  // the last tile reaches every key
+        return cost;
+    }
+    int64_t cost = 0;
+    for (int t = t0; t < t1; ++t) cost += plan_tile_cost(t, bm, L, Lk, wl, wr);
+    return cost;
+}
+
 // Keys visited by the query tiles [s * strip, min(nq, (s + 1) * strip)) of a segment.
 __device__ __forceinline__ int plan_strip_cost(int s, int strip, int nq, int bm, int L, int Lk, int wl, int wr) {
-    int64_t cost = 0;
-    for (int t = s * strip; t < min(nq, (s + 1) * strip); ++t) cost += plan_tile_cost(t, bm, L, Lk, wl, wr);
+    const int64_t cost = plan_tiles_cost(s * strip, min(nq, (s + 1) * strip), nq, bm, L, Lk, wl, wr);
     return (int)min(cost, (int64_t)0x7fffffff);
 }
 
 // Keys visited by all strips of a segment.
-__device__ __forceinline__ int plan_segment_cost(int ns, int strip, int nq, int bm, int L, int Lk, int wl, int wr) {
-    int64_t cost = 0;
-    for (int s = 0; s < ns; ++s) cost += plan_strip_cost(s, strip, nq, bm, L, Lk, wl, wr);
-    return (int)min(cost, (int64_t)0x7fffffff);
+__device__ __forceinline__ int plan_segment_cost(int nq, int bm, int L, int Lk, int wl, int wr) {
+    return (int)min(plan_tiles_cost(0, nq, nq, bm, L, Lk, wl, wr), (int64_t)0x7fffffff);
+}
+
+// Strips [s_lo, s_hi) whose tiles all visit the same number of keys: every full tile of a global
+// call, or the full tiles of a two-sided window that reach neither end of the keys
+// (cost bm + wl + wr). Empty (s_lo >= s_hi) for other shapes.
+__device__ __forceinline__ void plan_flat_strips(int strip, int bm, int L, int Lk, int wl, int wr, int &s_lo,
+                                                 int &s_hi) {
+    s_lo = s_hi = 0;
+    const bool global = wl < 0 && wr < 0, band = wl >= 0 && wr >= 0;
+    if (!global && !band) return;
+    const int off = Lk - L;
+    int t_lo = 0, t_hi = L / bm;  // full tiles: (t + 1) bm <= L
+    if (band) {
+        t_lo = wl - off > 0 ? (wl - off + bm - 1) / bm : 0;           // t bm + off >= wl
+        t_hi = L - wr > 0 ? min(t_hi, (L - wr) / bm) : 0;              // (t + 1) bm + off + wr <= Lk
+    }
+    s_lo = (t_lo + strip - 1) / strip;
+    s_hi = t_hi / strip;
 }
 
 __device__ __forceinline__ int plan_bucket(int cost) {
@@ -57,6 +90,7 @@ __device__ __forceinline__ int plan_bucket(int cost) {
 // C5's 256 segments of up to 32 strips took 40 us by waves against 13 us by threads.
 constexpr int kSerialStrips = 32;
 constexpr int kWaveQueue = 2048;
+constexpr int kCachedBounds = 4096;  // segments whose boundaries the plan keeps in LDS
 
 // One entry per strip of `strip` consecutive query tiles of `bm` rows: (segment, first tile,
 // the segment's first query row, its query rows), so a kernel reads a work item's bounds with
@@ -81,25 +115,38 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
     __shared__ int off[64];
     __shared__ int4 queue[kWaveQueue];  // (segment, query rows, keys, query start)
     __shared__ int queued;
+    __shared__ int cu_s[kCachedBounds + 1], cuk_s[kCachedBounds + 1];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+    // The boundaries are read from global memory once, into LDS (up to kCachedBounds segments):
+    // every later pass reads them there instead of paying a dependent global load each.
+    const bool cached = n_seq <= kCachedBounds;
+    if (cached) {
+        for (int i = tid; i <= n_seq; i += blockDim.x) {
+            cu_s[i] = cu[i];
+            cuk_s[i] = cuk[i];
+        }
+    }
     if (tid < 64) cnt[tid] = 0;
     if (tid == 0) queued = 0;
     __syncthreads();
+    auto bound = [&](int i) { return cached ? cu_s[i] : cu[i]; };
+    auto bound_k = [&](int i) { return cached ? cuk_s[i] : cuk[i]; };
 
+    // A segment with no query rows has nothing to plan; one outside the contract takes no entry.
     auto strips_of = [&](int seg, int &L, int &Lk, int &nq, int &ns) {
-        L = cu[seg + 1] - cu[seg];
-        Lk = cuk[seg + 1] - cuk[seg];
+        L = bound(seg + 1) - bound(seg);
+        Lk = bound_k(seg + 1) - bound_k(seg);
         nq = (L + bm - 1) / bm;
         ns = (nq + strip - 1) / strip;
-        if (L < 0 || Lk < 0 || L > max_seqlen || Lk > max_seqlen_k) return false;  // outside the contract
+        if (L <= 0 || Lk < 0 || L > max_seqlen || Lk > max_seqlen_k) return false;
         return max(L, Lk) > short_max;  // the tiled kernel's
     };
     for (int seg = tid; seg < n_seq; seg += blockDim.x) {
         int L, Lk, nq, ns;
         if (strips_of(seg, L, Lk, nq, ns) && ns > kSerialStrips) {
             const int qi = atomicAdd(&queued, 1);
-            if (qi < kWaveQueue) queue[qi] = make_int4(seg, L, Lk, cu[seg]);
+            if (qi < kWaveQueue) queue[qi] = make_int4(seg, L, Lk, bound(seg));
         }
     }
     __syncthreads();
@@ -111,7 +158,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
         int L, Lk, nq, ns;
         if (!strips_of(seg, L, Lk, nq, ns) || (by_wave && ns > kSerialStrips)) return;
         if (group) {
-            const int b = plan_bucket(plan_segment_cost(ns, strip, nq, bm, L, Lk, wl, wr));
+            const int b = plan_bucket(plan_segment_cost(nq, bm, L, Lk, wl, wr));
             if (!place) {
                 atomicAdd(&cnt[b], ns);
                 return;
@@ -120,18 +167,21 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t *cu, const int
             const int pos = atomicAdd(&off[b], ns);
             const bool rev =
                 plan_strip_cost(ns - 1, strip, nq, bm, L, Lk, wl, wr) > plan_strip_cost(0, strip, nq, bm, L, Lk, wl, wr);
-            const int start = cu[seg];
+            const int start = bound(seg);
             for (int i = 0; i < ns; ++i)
                 if (pos + i < cap) work[pos + i] = make_int4(seg, (rev ? ns - 1 - i : i) * strip, start, L);
             return;
         }
-        const int start = cu[seg];
+        const int start = bound(seg);
+        int s_lo, s_hi;  // strips of equal cost: a run crosses them in one step
+        plan_flat_strips(strip, bm, L, Lk, wl, wr, s_lo, s_hi);
         int s = 0;
         while (s < ns) {
             // A run of consecutive strips in one cost bucket gets one contiguous reservation.
             const int b = plan_bucket(plan_strip_cost(s, strip, nq, bm, L, Lk, wl, wr));
             int e = s + 1;
-            while (e < ns && plan_bucket(plan_strip_cost(e, strip, nq, bm, L, Lk, wl, wr)) == b) ++e;
+            while (e < ns && plan_bucket(plan_strip_cost(e, strip, nq, bm, L, Lk, wl, wr)) == b)
+                e = e >= s_lo && e < s_hi ? s_hi : e + 1;
             if (!place) {
                 atomicAdd(&cnt[b], e - s);
             } else {
