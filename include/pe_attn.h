@@ -98,7 +98,7 @@ typedef struct pe_attn_args {
     /* Kernel for the long segments of a bounded band window each of whose rows spans five
        32-key blocks (ModernBERT's +-64: floor((31 + right) / 32) + ceil(left / 32) == 4), with
        head_dim 64, an odd GQA ratio and no cu_seqlens_k: 0 the library's choice (the streaming
-       band kernel from 6144 query tiles of 128 rows x heads, the tiled kernel below), 1 the
+       band kernel from 17667 query tiles of 128 rows x heads, the tiled kernel below), 1 the
        streaming band kernel, 2 the tiled kernel. Other calls ignore it. */
     int32_t band_kernel;
     /* Host lower bound on every query segment length, or 0 when not known (flash_attn's

@@ -23,6 +23,11 @@ profiles/dispatch_sweep.md and re-derived by ``fit_boundary`` in the tests):
   lengths, per token.
 - head_dim 256 always runs the tiled kernel (the short kernel serves head_dim <= 128).
 
+The long segments of a call with a +-64-shaped band go to the tiled kernel or, on large calls,
+the streaming band kernel; that size rule is fitted by ``fit_band_rule`` to the band sweep
+(``python bench.py --band-sweep``, profiles/band_sweep.md) and is the C library's
+``kBandMinTiles`` / ``kBandStrip8Tiles``.
+
 Names the reference's callers consult are kept: ``AttentionWorkload`` (capture-safe batch
 statistics) and ``get_packed_inference_policy`` (the current device's calibrated policy, None
 where none is calibrated; crossovers are never borrowed from another GPU).
@@ -143,6 +148,38 @@ def fit_boundary(rows: Iterable[Mapping], head_dim: int, *, min_segments: int = 
         return total
 
     return min((0, *SHORT_CAPACITIES), key=lambda c: (cost(c), c))
+
+
+def fit_band_rule(rows: Iterable[Mapping]) -> tuple[int | None, int | None]:
+    """The library's size rule for +-64-shaped band calls, fitted to the band sweep
+    (``python bench.py --band-sweep``, profiles/band_sweep.md): ``(min_tiles, strip8_tiles)``,
+    the streaming band kernel from ``min_tiles`` query tiles (128 rows x heads) on, at strip 8
+    from ``strip8_tiles`` on and strip 4 below, the tiled kernel under ``min_tiles`` (None:
+    never). The pair has the least total time over the rows (columns ``query_tiles``,
+    ``tiled_us``, ``band4_us``, ``band8_us``); on equal totals the tiled kernel keeps more rows.
+    Each threshold is placed halfway (geometric mean, rounded) between the two measured tile
+    counts it separates, 0 when it precedes every row."""
+    rows = [dict(r) for r in rows]
+    counts = sorted({int(r["query_tiles"]) for r in rows})
+    if not counts:
+        return None, None
+    n = len(counts)
+
+    def cost(k: int, j: int) -> float:  # band from counts[k], strip 8 from counts[j] (n: never)
+        total = 0.0
+        for r in rows:
+            i = counts.index(int(r["query_tiles"]))
+            total += float(r["tiled_us"] if i < k else (r["band4_us"] if i < j else r["band8_us"]))
+        return total
+
+    k, j = min(((k, j) for k in range(n + 1) for j in range(k, n + 1)), key=lambda kj: (cost(*kj), -kj[0], kj[1]))
+
+    def place(i: int) -> int | None:
+        if i >= n:
+            return None
+        return 0 if i == 0 else round((counts[i - 1] * counts[i]) ** 0.5)
+
+    return place(k), (place(j) if k < n else None)
 
 
 # Fitted to profiles/dispatch_sweep.md (tests/test_host_cpu.py re-derives it from that table).

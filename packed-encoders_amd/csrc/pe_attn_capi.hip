@@ -153,11 +153,13 @@ int64_t query_tiles(const pe_attn_args *a) { return (int64_t)a->total_tokens / 1
 // Whether a call's long segments run the streaming band kernel (band64_attn_kernel) rather than
 // the tiled kernel: its window shape, one query head per kv head group, shared key segments,
 // and the caller's band_kernel choice; by default a call of at least kBandMinTiles query tiles.
-// Measured on gfx950 over C2-like document mixes and equal-length batches (12 heads, +-64):
-// the streaming kernel (two workgroups per CU, long-lived) is 3-13% faster from about 6K
-// tiles up and up to 20% slower on smaller calls, where the tiled kernel's short workgroups
-// (three per CU) balance the tail better.
-constexpr int64_t kBandMinTiles = 6144;
+// Both thresholds are fitted to a sweep of C2-like document mixes and equal-length batches
+// (12 heads, +-64; attention_dispatch.fit_band_rule): the tiled kernel's short-lived
+// workgroups (three per CU) win every call below about 13K tiles, the band kernel's strips
+// (two workgroups per CU, each key block staged once) win large document mixes by 1-6% from
+// about 24K tiles, at strip 8; the thresholds sit halfway (geometric) between those points.
+constexpr int64_t kBandMinTiles = 17667;
+constexpr int64_t kBandStrip8Tiles = 17667;
 bool uses_band64(const pe_attn_args *a) {
     const int wr = a->causal ? 0 : a->window_right;
     const bool shape = a->head_dim == 64 && !a->cu_seqlens_k && heads_per_tile(a) == 1 &&
@@ -167,12 +169,12 @@ bool uses_band64(const pe_attn_args *a) {
 }
 
 // Query tiles per tiled-kernel workgroup: the caller's choice, else the gfx950 default. The
-// band kernel streams its key blocks along a strip: 4 tiles, 8 on calls of 16K tiles or more
-// (measured best on the same sweep).
+// band kernel streams its key blocks along a strip: 8 tiles from kBandStrip8Tiles on, 4 on the
+// smaller calls that force it (band_kernel = 1).
 int effective_strip(const pe_attn_args *a) {
     if (a->strip > 0) return a->strip;
     if (!uses_band64(a)) return 1;
-    return query_tiles(a) >= 16384 ? 8 : 4;
+    return query_tiles(a) >= kBandStrip8Tiles ? 8 : 4;
 }
 
 AttnParams make_params(const pe_attn_args *a, int short_max) {

@@ -108,12 +108,13 @@ def test_band_kernel_every_admitted_window_class(pe, window, causal):
 
 def test_segment_across_the_size_rule(pe):
     """A +-64 segment alone (a small call: the tiled kernel) and the same segment packed into a
-    call of at least 6,144 query tiles (the band kernel) agree within the parity bar, not bit
-    for bit: the library's size rule is the one way a segment's bits depend on its batch."""
+    call of at least 17,667 query tiles (the band kernel) agree within the parity bar, not bit
+    for bit: besides the short-kernel boundary, the library's size rule is the one way a
+    segment's bits depend on its batch."""
     from packed_encoders_amd import _lib
 
     announce("segment alone (tiled) vs in a large call (band)")
-    lengths = [1000] + [4096] * 16
+    lengths = [1000] + [8192] * 24  # 18,432 query tiles at 12 heads
     q, k, v, cu, _ = _inputs(lengths, hq=12, seed=68)
     qd, kd, vd, cud = _dev(q, k, v, cu)
     mx = max(lengths)
@@ -195,8 +196,8 @@ def test_band_kernel_no_leakage_and_batch_independence(pe):
 
 
 def test_library_choice_by_call_size(pe):
-    """band_kernel=0 keeps the tiled kernel on a small call and takes the band kernel on a
-    large one; the large call matches the oracle on sampled rows."""
+    """band_kernel=0 keeps the tiled kernel on a small call and takes the band kernel (strip 8)
+    on a large one; the large call matches the oracle on sampled rows."""
     from oracle import attention as oa
     from packed_encoders_amd import _lib
 
@@ -205,11 +206,11 @@ def test_library_choice_by_call_size(pe):
     q, k, v, cu, _ = _inputs(small, hq=12, seed=65)
     qd, kd, vd, cud = _dev(q, k, v, cu)
     assert _kernel_of(qd, kd, cud, 512, (64, 64), 0)[0] == _lib.KERNEL_TILED
-    big = [4096] * 16  # 512 query tiles x 12 heads = 6144
+    big = [8192] * 24  # 1,536 query tiles x 12 heads = 18,432
     q, k, v, cu, _ = _inputs(big, hq=12, seed=66)
     qd, kd, vd, cud = _dev(q, k, v, cu)
-    assert _kernel_of(qd, kd, cud, 4096, (64, 64), 0) == (_lib.KERNEL_BAND64, 4)
-    got = _run(pe, qd, kd, vd, cud, 4096, (64, 64), band_kernel=0)
+    assert _kernel_of(qd, kd, cud, 8192, (64, 64), 0) == (_lib.KERNEL_BAND64, 8)
+    got = _run(pe, qd, kd, vd, cud, 8192, (64, 64), band_kernel=0)
     torch.cuda.synchronize()
     rows = np.linspace(0, sum(big) - 1, 96).astype(np.int64)
     f = lambda t: t.float().numpy()

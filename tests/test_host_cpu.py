@@ -301,6 +301,53 @@ def test_gfx950_boundaries_are_the_fit_of_the_committed_sweep():
     assert attention_dispatch.fit_boundary(rows, 64, min_segments=10 ** 6) == 0
 
 
+def _band_sweep_rows():
+    """The data table of profiles/band_sweep.md (the committed gfx950 band sweep)."""
+    import pathlib
+
+    text = (pathlib.Path(__file__).resolve().parents[1] / "profiles" / "band_sweep.md").read_text()
+    lines = [ln for ln in text.splitlines() if ln.startswith("|")]
+    header = next(i for i, ln in enumerate(lines) if ln.startswith("| batch | n_seq |"))
+    names = [c.strip() for c in lines[header].strip("|").split("|")]
+    rows = []
+    for ln in lines[header + 2:]:
+        cells = [c.strip() for c in ln.strip("|").split("|")]
+        rows.append({k: (v if k == "batch" else float(v)) for k, v in zip(names, cells)})
+    return rows
+
+
+def test_band_size_rule_is_the_fit_of_the_committed_sweep(pe):
+    """The C library's band-kernel thresholds (streaming band kernel from kBandMinTiles query
+    tiles, strip 8 from kBandStrip8Tiles) are what fit_band_rule derives from the committed
+    band sweep: one tile below the threshold a +-64 call runs the tiled kernel, at it the band
+    kernel at the fitted strip. The fit responds to the data."""
+    import ctypes
+
+    from packed_encoders_amd import _lib
+
+    rows = _band_sweep_rows()
+    assert len(rows) == 17
+    t, s8 = attention_dispatch.fit_band_rule(rows)
+    assert t is not None and s8 is not None and s8 >= t
+
+    def kernels(tiles):
+        a = _lib.AttnArgs()
+        a.struct_size = ctypes.sizeof(_lib.AttnArgs)
+        a.dtype, a.head_dim, a.n_heads_q, a.n_heads_kv = 1, 64, 1, 1
+        a.n_seq, a.total_tokens, a.max_seqlen = 1, tiles * 128, tiles * 128
+        a.softmax_scale, a.window_left, a.window_right, a.short_max = 0.125, 64, 64, -1
+        out = (ctypes.c_int32 * 6)()
+        assert _lib.library().pe_attn_kernels(ctypes.byref(a), out) == 0
+        return out[1], out[2]
+
+    assert kernels(t - 1) == (_lib.KERNEL_TILED, 1)
+    assert kernels(t) == (_lib.KERNEL_BAND64, 8 if t >= s8 else 4)
+    assert kernels(s8) == (_lib.KERNEL_BAND64, 8)
+    # a free band kernel takes every row; a free tiled kernel none
+    assert attention_dispatch.fit_band_rule([dict(r, band8_us=0.0) for r in rows]) == (0, 0)
+    assert attention_dispatch.fit_band_rule([dict(r, tiled_us=0.0) for r in rows]) == (None, None)
+
+
 # ----------------------------------------------------------------------------- pieces
 
 

@@ -10,7 +10,11 @@ under the same routing boundary (``short_max`` 64: a segment's kernel follows it
 The library's default boundary is keyed on the batch's longest segment (every segment short
 when it is at most 128 tokens), so with the default a 65-128-token segment may take the short
 kernel alone and the tiled kernel in a longer batch: both within tolerance, not the same bits,
-as the reference's per-batch Triton / FlashAttention choice.
+as the reference's per-batch Triton / FlashAttention choice. The one other exception is the
++-64-shaped band's size rule: a call of at least 17,667 query tiles (128 rows x heads) runs its
+long segments in the streaming band kernel, a smaller one in the tiled kernel, so such a segment
+alone and inside a large call agree within tolerance, not bit for bit
+(tests/test_band_kernel_gpu.py::test_segment_across_the_size_rule checks that bound).
 """
 
 from __future__ import annotations

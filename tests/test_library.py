@@ -265,9 +265,10 @@ def test_short_kernel_heads_per_workgroup(lib):
 
 def test_kernel_choice_per_call(lib):
     """pe_attn_kernels reports (short capacity, long-segment kernel, strip, tile rows): the
-    global head_dim 64 kernel, the tiled kernel for small band calls and the streaming band
-    kernel from 6144 query tiles (strip 4, 8 from 16384), band_kernel overriding the size
-    rule only where the window shape, an odd GQA ratio and shared key segments allow it."""
+    global head_dim 64 kernel, the tiled kernel for band calls below 17667 query tiles and the
+    streaming band kernel from there (strip 8; strip 4 when forced on a smaller call),
+    band_kernel overriding the size rule only where the window shape, an odd GQA ratio and
+    shared key segments allow it."""
     from packed_encoders_amd import _lib
 
     band = dict(window_left=64, window_right=64)
@@ -275,10 +276,11 @@ def test_kernel_choice_per_call(lib):
     assert _kernels(lib, **band) == (64, _lib.KERNEL_TILED, 1, 128)  # C2: 3041 tiles
     assert _kernels(lib, band_kernel=1, **band) == (64, _lib.KERNEL_BAND64, 4, 128)
     c4 = dict(n_seq=16, total_tokens=131072, max_seqlen=8192, n_heads_q=16, n_heads_kv=16)
-    assert _kernels(lib, **c4, **band) == (64, _lib.KERNEL_BAND64, 8, 128)  # 16384 tiles
-    assert _kernels(lib, **c4, band_kernel=2, **band) == (64, _lib.KERNEL_TILED, 1, 128)
-    mid = dict(n_seq=128, total_tokens=67493, max_seqlen=4000)  # 6327 tiles
-    assert _kernels(lib, **mid, **band) == (64, _lib.KERNEL_BAND64, 4, 128)
+    assert _kernels(lib, **c4, **band) == (64, _lib.KERNEL_TILED, 1, 128)  # 16384 tiles
+    assert _kernels(lib, **c4, band_kernel=1, **band) == (64, _lib.KERNEL_BAND64, 4, 128)
+    big = dict(n_seq=512, total_tokens=253948, max_seqlen=2048)  # 23796 tiles
+    assert _kernels(lib, **big, **band) == (64, _lib.KERNEL_BAND64, 8, 128)
+    assert _kernels(lib, **big, band_kernel=2, **band) == (64, _lib.KERNEL_TILED, 1, 128)
     assert _kernels(lib, band_kernel=1, n_heads_q=12, n_heads_kv=4, **band)[1] == _lib.KERNEL_BAND64  # GQA 3:1
     assert _kernels(lib, band_kernel=1, n_heads_q=12, n_heads_kv=6, **band)[1] == _lib.KERNEL_TILED  # GQA 2:1
     assert _kernels(lib, band_kernel=1, window_left=5, window_right=7)[1] == _lib.KERNEL_TILED
