@@ -18,9 +18,10 @@ schedule on the host's cores with the reference's own CPU kernel (oracle/_ref) f
 short-global layers and per-segment fp32 torch SDPA for global layers longer than 128 (the
 reference's rule).
 
-For C2 the line also carries ``end_to_end``: the whole packed ModernBERT-base forward
+For C2 and C1 the line also carries ``end_to_end``: the whole packed ModernBERT-base forward
 (random-init weights, bf16) over the same batch through ``pe.pack``, eager and replayed from
-the bucketed HIP-graph runner, in tokens/s.
+the bucketed HIP-graph runner, in tokens/s (C1's short batch is the launch-bound case graphs
+exist for).
 
 Before the W warm-up steps the step runs untimed for ``--settle`` seconds (0.3 by default,
 reported as ``settle_s``): an idle MI355X measures up to 10% slower over its first ~10 ms of
@@ -369,7 +370,7 @@ def model_bench(args, workload):
     ids = torch.randint(0, cfg.vocab_size, (sum(lengths),), device=dev, generator=g)
     cu = torch.tensor(workload.cu_seqlens(), dtype=torch.int32, device=dev)
     positions = torch.cat([torch.arange(n, device=dev) for n in lengths])
-    batch = pe.PackedBatch(ids, cu, max(lengths), positions)
+    batch = pe.PackedBatch(ids, cu, max(lengths), positions, host_lengths=tuple(lengths))  # as a collator gives
     gcfg = pe.GraphConfig(max_batch=len(lengths), max_seq=max(lengths), pad_to=256, warmup=2)
     pe.pack(model, attention_backend="hip", cuda_graph=gcfg, validate=False)
     engine = pe.get_engine(model)
@@ -899,6 +900,79 @@ def band_sweep(reps: int = 10, replays: int = 5) -> int:
     return 0
 
 
+def graph_overhead(repeats: int = 7) -> int:
+    """What a HIP-graph replay costs beside eager launches on this stack. Nodes: the C1
+    attention call (one short-kernel launch, about 7 us of kernel) and, as a control, a torch
+    elementwise kernel on one element (about 2 us). For N = 1..64 nodes captured into one graph,
+    the replay's time per replay (HIP events on the replaying stream, median of ``repeats``
+    samples of 50 replays) against N eager launches of the same work; a least-squares line
+    through the replay times separates the fixed cost of a replay from the cost of each node.
+    Prints one JSON line per node kind; the committed summary is profiles/graph_overhead.md."""
+    import torch
+
+    import packed_encoders_amd as pe
+    from packed_encoders_amd import _lib, hip_attention as hip
+
+    lib = _lib.library()
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.Stream(dev)
+    wl = pe.workloads.c1()
+    T, h, d = wl.total_tokens, wl.n_heads_q, wl.head_dim
+    gen = torch.Generator(device=dev).manual_seed(3)
+    q, k, v = (torch.randn(T, h, d, device=dev, generator=gen, dtype=torch.bfloat16) for _ in range(3))
+    out = torch.empty_like(q)
+    cu = torch.tensor(wl.cu_seqlens(), dtype=torch.int32, device=dev)
+    a = hip._args(q, k, v, out, cu, wl.max_seqlen, wl.scale, -1, -1, False, None, -1)
+    tiny = torch.zeros(1, device=dev)
+
+    def attention():
+        assert lib.pe_attn_short_fwd(ctypes.byref(a), torch.cuda.current_stream(dev).cuda_stream) == 0
+
+    def elementwise():
+        tiny.add_(1.0)
+
+    def per_call_us(fn, n, reps=50) -> float:
+        samples = []
+        for _ in range(repeats):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(torch.cuda.current_stream(dev))
+            for _ in range(reps):
+                fn()
+            e1.record(torch.cuda.current_stream(dev))
+            torch.cuda.synchronize()
+            samples.append(e0.elapsed_time(e1) * 1e3 / reps)
+        return statistics.median(samples)
+
+    for kind, node in (("c1_attention", attention), ("elementwise_1", elementwise)):
+        rows = []
+        for n in (1, 2, 4, 8, 16, 32, 64):
+            with torch.cuda.stream(stream):
+                for _ in range(3):
+                    node()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for _ in range(n):
+                    node()
+            graph.replay()
+            torch.cuda.synchronize()
+            replay = per_call_us(graph.replay, n)
+            eager = per_call_us(lambda: [node() for _ in range(n)], n)
+            rows.append({"nodes": n, "replay_us": round(replay, 2), "eager_us": round(eager, 2)})
+            del graph
+        xs, ys = [r["nodes"] for r in rows], [r["replay_us"] for r in rows]
+        mx, my = statistics.mean(xs), statistics.mean(ys)
+        slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+        ex = [r["eager_us"] for r in rows]
+        me = statistics.mean(ex)
+        slope_e = sum((x - mx) * (y - me) for x, y in zip(xs, ex)) / sum((x - mx) ** 2 for x in xs)
+        print(json.dumps({"node": kind, "rows": rows,
+                          "replay_fixed_us": round(my - slope * mx, 2), "replay_per_node_us": round(slope, 3),
+                          "eager_fixed_us": round(me - slope_e * mx, 2), "eager_per_call_us": round(slope_e, 3)}),
+              flush=True)
+    return 0
+
+
 def dispatch_sweep(reps: int = 20, replays: int = 5) -> int:
     """Short kernel vs tiled kernel per segment length: the measurement the gfx950 routing
     boundary (attention_dispatch.HipDispatchPolicy) is fitted to. For head_dim 64 (12 heads)
@@ -984,6 +1058,8 @@ def main() -> int:
                     help="only time the short kernel against the tiled kernel per segment length")
     ap.add_argument("--band-sweep", action="store_true",
                     help="only time the streaming band kernel against the tiled kernel on +-64 calls of every size")
+    ap.add_argument("--graph-overhead", action="store_true",
+                    help="only measure a HIP-graph replay's fixed and per-node cost against eager launches")
     ap.add_argument("--peaks", action="store_true",
                     help="only measure this card's achieved bf16 MFMA, HBM read/copy and global-to-LDS rates")
     ap.add_argument("--profile-commands", action="store_true",
@@ -1012,6 +1088,8 @@ def main() -> int:
         return band_sweep()
     if args.peaks:
         return peaks()
+    if args.graph_overhead:
+        return graph_overhead()
 
     import packed_encoders_amd as pe
 
@@ -1019,7 +1097,7 @@ def main() -> int:
     workload = WORKLOADS[w]()
     res = gpu_bench(args, workload)
     model_res = None
-    if w == "C2" and not args.no_model:
+    if w in ("C1", "C2") and not args.no_model:
         try:
             model_res = model_bench(args, workload)
         except Exception as exc:  # reported, never required

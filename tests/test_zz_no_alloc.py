@@ -62,3 +62,92 @@ def test_noalloc_matches_workspace_entry_point_on_two_calls(pe, d, hq, hkv, wind
         got = _call(lib, "noalloc", q, k, v, cu, max(lengths), window, causal, gt)
         assert torch.isfinite(got).all()
         assert torch.equal(got, want), f"call {call}: noalloc output differs from the workspace entry point"
+
+
+def _inputs(T, hq, hkv, d, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(T, h, d, generator=g).bfloat16().cuda() for h in (hq, hkv, hkv)]
+
+
+def test_noalloc_captured_replays_follow_rewritten_lengths(pe):
+    """The no-allocation call captured once in a HIP graph (after an eager call on this device)
+    and replayed while cu_seqlens is rewritten in place between replays: every replay re-plans
+    from the static array and matches the workspace entry point run eagerly on the same lengths,
+    bit for bit (the graph holds no memset: the plan writes every count it reads)."""
+    from packed_encoders_amd import _lib
+    from packed_encoders_amd.hip_attention import _args
+
+    lib = _lib.library()
+    T, max_seqlen = 2000, 1500
+    q, k, v = _inputs(T, 12, 12, 64, seed=71)
+    batches = ([700, 40, 900, 300, 60], [100, 1500, 64, 36, 300], [2, 998, 1000, 0, 0])
+    cus = [torch.tensor([0, *np.cumsum(b).tolist()], dtype=torch.int32, device="cuda") for b in batches]
+    cu = cus[0].clone()
+    out = torch.zeros(T, 12, 64, dtype=torch.bfloat16, device="cuda")
+    a = _args(q, k, v, out, cu, max_seqlen, 0.125, -1, -1, False, None, -1)
+    announce("noalloc eager call before capture")
+    assert lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(a), torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    announce("noalloc capture")
+    with torch.cuda.graph(graph, stream=side):
+        assert lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(a), torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for i in (0, 1, 2, 0, 1):
+        announce(f"noalloc replay with lengths {batches[i]}")
+        cu.copy_(cus[i])
+        out.fill_(3.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _call(lib, "workspace", q, k, v, cus[i], max_seqlen, (-1, -1), False, None)
+        n = int(cus[i][-1])
+        assert torch.equal(out[:n], want[:n]), f"replay with lengths {batches[i]} differs"
+    del graph
+
+
+_CHILD = r"""
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+import torch
+import packed_encoders_amd as pe
+from packed_encoders_amd import _lib
+from packed_encoders_amd.hip_attention import _args
+lib = _lib.library()
+g = torch.Generator().manual_seed(5)
+q, k, v = (torch.randn(900, 4, 64, generator=g).bfloat16().cuda() for _ in range(3))
+cu = torch.tensor([0, 300, 340, 900], dtype=torch.int32, device="cuda")
+out = torch.zeros_like(q)
+a = _args(q, k, v, out, cu, 560, 0.125, -1, -1, False, None, -1)
+graph = torch.cuda.CUDAGraph()
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+with torch.cuda.graph(graph, stream=side):  # the library's first no-allocation call on this device
+    rc = lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(a), torch.cuda.current_stream().cuda_stream)
+torch.cuda.current_stream().wait_stream(side)
+print("capture rc", rc, flush=True)
+assert rc == 0, rc
+graph.replay()
+torch.cuda.synchronize()
+with torch.inference_mode():
+    want = pe.varlen_attention(q, k, v, cu, 560, softmax_scale=0.125)
+torch.cuda.synchronize()
+assert torch.equal(out, want)
+print("CHILD_OK", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_capture(pe):
+    """In a fresh process whose first no-allocation call is made inside a graph capture (the
+    static array's per-device address looked up while capturing), the captured call replays to
+    the same bits as the workspace path."""
+    import subprocess
+    import sys
+
+    from conftest import ROOT
+
+    announce("noalloc first call inside capture (child process)")
+    proc = subprocess.run([sys.executable, "-c", _CHILD, str(ROOT)], capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0 and "CHILD_OK" in proc.stdout, proc.stdout[-2000:] + proc.stderr[-2000:]
