@@ -191,9 +191,9 @@ LARGE_LOGIT_CASES = {
     "causal": (LARGE_LOGIT_LONG, 64, 4, (-1, -1), True, 0, 0),
     "d128": (LARGE_LOGIT_LONG, 128, 4, (-1, -1), False, 0, 0),
     "d256-causal": (LARGE_LOGIT_LONG, 256, 2, (-1, -1), True, 0, 0),
-    # 520 segments of 1..64 tokens: the short kernel with four heads per workgroup (it keeps
-    # four while segments x head groups fill two workgroups per CU)
-    "short-4heads": ([1 + (7 * i) % 64 for i in range(520)], 64, 4, (-1, -1), False, 64, 0),
+    # 2,080 segments of 1..64 tokens: the short kernel with four heads per workgroup (it keeps
+    # four while segments x head groups fill eight workgroups per CU)
+    "short-4heads": ([1 + (7 * i) % 64 for i in range(2080)], 64, 4, (-1, -1), False, 64, 0),
 }
 
 

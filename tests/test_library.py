@@ -250,14 +250,16 @@ def _kernels(lib, short=False, **kw):
 
 def test_short_kernel_heads_per_workgroup(lib):
     """pe_attn_kernels reports the short kernel's heads per workgroup and its workgroups: the
-    shape's default (pe_attn_short_config) halved while the batch would give fewer than two
-    workgroups per CU (512 on 256 CUs), so a small batch spreads over more CUs."""
+    shape's default (pe_attn_short_config) halved while the batch would give fewer than eight
+    workgroups per CU (2,048 on 256 CUs), so a small batch spreads over more, smaller workgroups."""
     q = dict(max_seqlen=64, total_tokens=1307)
     assert _kernels(lib, short=True, n_seq=32, **q) == (1, 32 * 12)  # C1
-    assert _kernels(lib, short=True, n_seq=100, **q) == (2, 100 * 6)
-    assert _kernels(lib, short=True, n_seq=171, **q) == (4, 171 * 3)
+    assert _kernels(lib, short=True, n_seq=100, **q) == (1, 100 * 12)
+    assert _kernels(lib, short=True, n_seq=342, **q) == (2, 342 * 6)
+    assert _kernels(lib, short=True, n_seq=683, **q) == (4, 683 * 3)
+    assert _kernels(lib, short=True, n_seq=576, max_seqlen=2000, total_tokens=60000) == (2, 576 * 6)  # C3
     assert _kernels(lib, short=True, n_seq=4096, max_seqlen=64, total_tokens=164139) == (4, 4096 * 3)  # Q4096
-    assert _kernels(lib, short=True, n_seq=300, max_seqlen=128, total_tokens=20000) == (2, 300 * 6)
+    assert _kernels(lib, short=True, n_seq=300, max_seqlen=128, total_tokens=20000) == (1, 300 * 12)
     assert _kernels(lib, short=True, head_dim=128, n_seq=4096, max_seqlen=128, total_tokens=300000) == (1, 4096 * 12)
     assert _kernels(lib, short=True, head_dim=128, n_seq=40, max_seqlen=32, total_tokens=800) == (1, 40 * 12)
     assert _kernels(lib, short=True, head_dim=256, n_heads_q=8, n_heads_kv=2) == (0, 0)
