@@ -89,7 +89,7 @@ def test_packed_short_attention_matches_oracle(pe, lengths, half_window):
     assert mean < 4e-3
 
 
-SHORT_HEADS = [(64, 12, 32, 1), (64, 12, 100, 2), (64, 12, 200, 4), (128, 6, 40, 1), (128, 6, 200, 2)]
+SHORT_HEADS = [(64, 12, 32, 1), (64, 12, 400, 2), (64, 12, 700, 4), (128, 6, 40, 1), (128, 6, 700, 2)]
 
 
 @pytest.mark.parametrize("d,hq,n_seq,heads", SHORT_HEADS, ids=[f"d{c[0]}_{c[2]}seg" for c in SHORT_HEADS])
