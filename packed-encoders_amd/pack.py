@@ -114,16 +114,20 @@ def _make_forward(encoder: nn.Module, state: PatchState):
     return patched
 
 
+# Hugging Face forward arguments the packed path does not serve: (argument, whether a value
+# uses it, what the error names). The messages are the reference's, which callers may match.
+_UNSERVED = (
+    ("inputs_embeds", lambda value: value is not None, "inputs_embeds"),
+    ("output_attentions", bool, "output_attentions"),
+    ("output_hidden_states", bool, "output_hidden_states"),
+    ("token_type_ids", lambda value: value is not None and bool(value.any()), "non-zero token_type_ids"),
+)
+
+
 def _reject_unsupported(kwargs: dict) -> None:
-    if kwargs.get("inputs_embeds") is not None:
-        raise NotImplementedError("packed-encoders does not support inputs_embeds")
-    if kwargs.get("output_attentions"):
-        raise NotImplementedError("packed-encoders does not support output_attentions")
-    if kwargs.get("output_hidden_states"):
-        raise NotImplementedError("packed-encoders does not support output_hidden_states")
-    token_type_ids = kwargs.get("token_type_ids")
-    if token_type_ids is not None and bool(token_type_ids.any()):
-        raise NotImplementedError("packed-encoders does not support non-zero token_type_ids")
+    for argument, used, what in _UNSERVED:
+        if used(kwargs.get(argument)):
+            raise NotImplementedError(f"packed-encoders does not support {what}")
 
 
 def _enable_graphs(encoder: nn.Module, state: PatchState, cuda_graph, seq_cutoff: int | None) -> None:

@@ -326,9 +326,11 @@ def probe_prefixed(prefixed, *, n_heads, n_kv_heads, head_dim, device, dtype, wi
     return (got.double() - want).abs().max().item()
 
 
-def _reason(exc: Exception) -> str:
-    first = str(exc).splitlines()[0][:160] if str(exc) else ""
-    return f"{type(exc).__name__}: {first}"
+def _why(exc: BaseException) -> str:
+    """One line naming why a candidate was rejected: the exception's type and the start of its
+    message."""
+    message = next(iter(str(exc).splitlines()), "")
+    return type(exc).__name__ + (f": {message[:160]}" if message else "")
 
 
 def _measure(fn: Callable[[], float]) -> tuple[float | None, str | None]:
@@ -336,10 +338,22 @@ def _measure(fn: Callable[[], float]) -> tuple[float | None, str | None]:
     try:
         err = fn()
     except Exception as exc:  # noqa: BLE001 - a failure to build or launch rejects the candidate
-        return None, _reason(exc)
+        return None, _why(exc)
     if not err < PROBE_TOLERANCE:
         return None, f"mismatch vs the float64 oracle: max abs err {err:.3g}"
     return err, None
+
+
+def _first_passing(tries: Sequence[tuple[str, Callable[[], float]]],
+                   rejected: dict[str, str]) -> tuple[str, float] | None:
+    """The first (label, probe) whose probe passes, as (label, error); every failure is recorded
+    in ``rejected`` under its label."""
+    for label, run in tries:
+        err, why = _measure(run)
+        if why is None:
+            return label, err
+        rejected[label] = why
+    return None
 
 
 def select_attention(*, n_heads: int, n_kv_heads: int, head_dim: int, causal: bool, device: torch.device,
@@ -356,30 +370,31 @@ def select_attention(*, n_heads: int, n_kv_heads: int, head_dim: int, causal: bo
     geometry = dict(n_heads=n_heads, n_kv_heads=n_kv_heads, head_dim=head_dim, device=device, dtype=dtype,
                     window=window, scale=scale)
     rejected: dict[str, str] = {}
-    for name in order or default_order(device):
-        forms: tuple[Callable, ...] = ()
-        try:
-            forms = _CANDIDATES[name](window, scale)
-        except Exception as exc:  # noqa: BLE001
-            rejected[name] = _reason(exc)
-            continue
-        packed, padded, prefixed = forms
-        err, why = _measure(lambda: probe(packed, padded, causal=causal, **geometry))
-        if why is not None:
-            rejected[name] = why
-            continue
-        choice = AttentionChoice(name=name, packed=packed, padded=padded, max_abs_err=err, rejected=rejected,
-                                 window=window, scale=scale)
-        if causal:
-            masks = (True, False) if bidirectional_prefixed else (True,)
-            for pname, fn in ((name, prefixed), ("sdpa", _sdpa(window, scale)[2])):
-                perr, why = _measure(lambda: max(probe_prefixed(fn, causal=c, **geometry) for c in masks))
-                if why is None:
-                    choice.prefixed, choice.prefixed_name, choice.prefixed_max_abs_err = fn, pname, perr
-                    break
-                rejected[f"{pname}:prefixed"] = why
-        return choice
-    raise ValidationError(f"no attention candidate passed: {rejected}")
+    built: dict[str, tuple[Callable, ...]] = {}
+
+    def build(name: str) -> float:  # the candidate's forms, then its packed/padded probe
+        built[name] = _CANDIDATES[name](window, scale)
+        packed, padded, _ = built[name]
+        return probe(packed, padded, causal=causal, **geometry)
+
+    winner = _first_passing([(name, lambda name=name: build(name)) for name in (order or default_order(device))],
+                            rejected)
+    if winner is None:
+        raise ValidationError(f"no attention candidate passed: {rejected}")
+    name, err = winner
+    packed, padded, prefixed = built[name]
+    choice = AttentionChoice(name=name, packed=packed, padded=padded, max_abs_err=err, rejected=rejected,
+                             window=window, scale=scale)
+    if causal:
+        masks = (True, False) if bidirectional_prefixed else (True,)
+        fallbacks = {f"{name}:prefixed": prefixed, "sdpa:prefixed": _sdpa(window, scale)[2]}
+        found = _first_passing([(label, lambda fn=fn: max(probe_prefixed(fn, causal=c, **geometry) for c in masks))
+                                for label, fn in fallbacks.items()], rejected)
+        if found is not None:
+            label, perr = found
+            choice.prefixed, choice.prefixed_name = fallbacks[label], label.split(":")[0]
+            choice.prefixed_max_abs_err = perr
+    return choice
 
 
 def sigmoid_gate(o: Tensor, gate: Tensor) -> Tensor:
