@@ -306,11 +306,13 @@ def _band_sweep_rows():
     import pathlib
 
     text = (pathlib.Path(__file__).resolve().parents[1] / "profiles" / "band_sweep.md").read_text()
-    lines = [ln for ln in text.splitlines() if ln.startswith("|")]
+    lines = text.splitlines()
     header = next(i for i, ln in enumerate(lines) if ln.startswith("| batch | n_seq |"))
     names = [c.strip() for c in lines[header].strip("|").split("|")]
     rows = []
     for ln in lines[header + 2:]:
+        if not ln.startswith("|"):
+            break  # the table ends at its first non-row line
         cells = [c.strip() for c in ln.strip("|").split("|")]
         rows.append({k: (v if k == "batch" else float(v)) for k, v in zip(names, cells)})
     return rows
