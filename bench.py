@@ -973,6 +973,89 @@ def graph_overhead(repeats: int = 7) -> int:
     return 0
 
 
+def compare_libraries(args, paths: list[str]) -> int:
+    """Interleaved medians of one layer's long-segment stage (or its short pass, or its plan)
+    across library builds: the in-tree ``libpe_attn.so`` first, then each build in ``paths``
+    (the same C ABI, compiled from modified sources). Every build plans and runs the same call
+    on the same inputs, cycling over ``--sets`` distinct Q/K/V sets; their outputs are checked
+    bit for bit against the first build's (a change that alters a result is reported). Then
+    ``--samples`` rounds, each timing ``--steps`` calls of every build in turn with HIP events,
+    so a build's median is never taken on a different stretch of the box's clock than
+    another's. This is how keep-or-drop decisions are made."""
+    import torch
+
+    from packed_encoders_amd import _build, _lib, hip_attention as hip, workloads as W
+    from packed_encoders_amd.attention_dispatch import hip_short_max
+
+    workload = WORKLOADS[args.workload]()
+    layer = workload.layers[0] if args.window is None else {"global": W.GLOBAL, "band": W.BAND64}[args.window]
+    dev = torch.device("cuda", 0)
+    T, hq, hkv, d = workload.total_tokens, workload.n_heads_q, workload.n_heads_kv, workload.head_dim
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    sets = []
+    for _ in range(max(1, args.sets)):
+        q, k, v = (torch.randn(T, h, d, device=dev, generator=gen, dtype=torch.bfloat16) for h in (hq, hkv, hkv))
+        g = torch.randn(T, hq, d, device=dev, generator=gen, dtype=torch.bfloat16) if layer.gate else None
+        sets.append((q, k, v, g))
+    cu = torch.tensor(workload.cu_seqlens(), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    A = ctypes.POINTER(_lib.AttnArgs)
+    stage = args.compare_stage
+    short_max = (hip_short_max(d, max_seqlen=workload.max_seqlen) if args.short_max is None else args.short_max)
+    builds = []
+    for path in [str(_build.LIBRARY), *paths]:
+        lib = ctypes.CDLL(path)
+        for name in ("pe_attn_plan", "pe_attn_tiled_fwd"):
+            getattr(lib, name).argtypes = [A, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.pe_attn_short_fwd.argtypes = [A, ctypes.c_void_p]
+        lib.pe_attn_workspace_size.argtypes = [A, ctypes.POINTER(ctypes.c_size_t)]
+        outs = [torch.zeros(T, hq, d, device=dev, dtype=torch.bfloat16) for _ in sets]
+        shortest = 0 if stage == "short" or args.no_min_seqlen else min(workload.lengths)
+        argl = [hip._args(q, k, v, o, cu, workload.max_seqlen, workload.scale, layer.window[0], layer.window[1],
+                          layer.causal, g, short_max, args.strip, min_seqlen=shortest)
+                for (q, k, v, g), o in zip(sets, outs)]
+        size = ctypes.c_size_t()
+        assert lib.pe_attn_workspace_size(ctypes.byref(argl[0]), ctypes.byref(size)) == 0
+        ws = torch.zeros(max(1, size.value), dtype=torch.uint8, device=dev)
+        counter = [0]
+
+        def call(lib=lib, argl=argl, ws=ws, n=size.value, counter=counter):
+            a = ctypes.byref(argl[counter[0] % len(argl)])
+            counter[0] += 1
+            if stage == "short":
+                rc = lib.pe_attn_short_fwd(a, stream)
+            elif stage == "plan":
+                rc = lib.pe_attn_plan(a, ws.data_ptr(), n, stream)
+            else:
+                rc = lib.pe_attn_tiled_fwd(a, ws.data_ptr(), n, stream)
+            assert rc == 0, rc
+
+        assert lib.pe_attn_plan(ctypes.byref(argl[0]), ws.data_ptr(), size.value, stream) == 0
+        for _ in argl:
+            call()
+        builds.append((path, call, outs[0]))
+    torch.cuda.synchronize()
+    results = {}
+    for path, _, out in builds:
+        results[path] = {"bit_identical_to_first": bool(torch.equal(out, builds[0][2])), "us": []}
+    settle(lambda: [b[1]() for b in builds], args.settle)
+    for _ in range(args.samples):
+        for path, call, _ in builds:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                call()
+            e1.record()
+            torch.cuda.synchronize()
+            results[path]["us"].append(round(e0.elapsed_time(e1) * 1e3 / args.steps, 2))
+    for path, r in results.items():
+        r["median_us"] = statistics.median(r["us"])
+    print(json.dumps({"compare": workload.name, "layer": {"window": layer.window, "causal": layer.causal,
+                                                          "gate": layer.gate},
+                      "stage": stage, "sets": len(sets), "results": results}), flush=True)
+    return 0
+
+
 def dispatch_sweep(reps: int = 20, replays: int = 5) -> int:
     """Short kernel vs tiled kernel per segment length: the measurement the gfx950 routing
     boundary (attention_dispatch.HipDispatchPolicy) is fitted to. For head_dim 64 (12 heads)
@@ -1058,6 +1141,14 @@ def main() -> int:
                     help="only time the short kernel against the tiled kernel per segment length")
     ap.add_argument("--band-sweep", action="store_true",
                     help="only time the streaming band kernel against the tiled kernel on +-64 calls of every size")
+    ap.add_argument("--compare", nargs="+", metavar="LIB",
+                    help="only time one layer call of --workload across library builds (the in-tree one first), "
+                         "interleaved, --samples rounds of --steps calls each")
+    ap.add_argument("--compare-stage", choices=("long", "short", "plan"), default="long",
+                    help="which stage --compare times (default: the long-segment kernel)")
+    ap.add_argument("--window", choices=("global", "band"), default=None,
+                    help="--compare: the layer's window (default: the workload's first layer)")
+    ap.add_argument("--sets", type=int, default=4, help="--compare: distinct Q/K/V sets cycled over (default 4)")
     ap.add_argument("--graph-overhead", action="store_true",
                     help="only measure a HIP-graph replay's fixed and per-node cost against eager launches")
     ap.add_argument("--peaks", action="store_true",
@@ -1090,6 +1181,8 @@ def main() -> int:
         return peaks()
     if args.graph_overhead:
         return graph_overhead()
+    if args.compare:
+        return compare_libraries(args, args.compare)
 
     import packed_encoders_amd as pe
 
