@@ -11,6 +11,16 @@
 // so a wave reads 8 LDS bytes per lane and MFMA where 32-row waves read 16, and the per-block
 // control is paid once per 16 MFMAs.
 //
+// Split tiles. A segment's last query tile often holds rows for at most half of a head's
+// waves (G = 1, a 300-token segment: tiles of 256 and 44 rows). Such a tile is split by key
+// block instead of leaving waves idle: waves rb and rb + WPH / 2 of a head take the same 64
+// rows, the first every key tile's first 32-key block and the second its second, each with its
+// own running maximum, sums and accumulators, merged through LDS at the end of the tile. Each
+// step then costs a wave half a full step's MFMAs and softmax. Only segments of more than 128
+// keys split: below that the merge's four barriers cost more than the shorter steps save
+// (measured on equal-length batches of 8 to 128 tokens). Whether a tile splits depends on its
+// segment's lengths alone.
+//
 // Staging is the ring of tiled_attn_kernel: NS = 3 stages of one 64-key K tile and one V tile
 // (16 KB), filled by direct global-to-LDS loads issued two steps ahead, out of the compiler's
 // sight, completion waited for with one constant s_waitcnt vmcnt per step; the 64 query rows
@@ -64,6 +74,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     constexpr int D = 64, BN = 64, NS = 3;
     constexpr int WPH = 4 / G;     // waves per query head
     constexpr int BM = 64 * WPH;   // query rows per query tile
+    constexpr int HALF = WPH > 1 ? WPH / 2 : 1;
     constexpr int CPR = D / 8;     // 16-byte units per K/V/Q row
     constexpr int TILE = BN * D;   // elements of one K (or V) tile
     constexpr int LPS = 4;         // 16-byte loads per lane and step: K 2 + V 2, or Q 4
@@ -71,6 +82,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     constexpr uint32_t kQWaveBytes = 32 * D * 2;  // a wave's 32 query rows of one Q step
 
     __shared__ __attribute__((aligned(16))) __bf16 ring[NS][2][TILE];
+    // A split tile's helper waves hand their row maxima and sums to the primaries here (their
+    // accumulators go through the ring stage the tile's last step freed).
+    __shared__ float merge_ml[2][4][64];
 
     const int item = blockIdx.x;
     const int entry = item / p.hgroups;
@@ -93,6 +107,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int wave = uniform(tid >> 6);
     const int col = lane & 31, kg = lane >> 5;
     const int slot = wave / WPH, rb = wave - slot * WPH;
+    // Split tiles (see the header): split_block(qt) is this wave's key block (0 or 1) in query
+    // tile qt when the tile splits, else -1; row_group(qt) the 64-row group the wave computes.
+    auto split_block = [&](int qt) {
+        const int groups = (L - qt * BM + 63) / 64;
+        return WPH >= 2 && Lk > 2 * BN && 2 * groups <= WPH ? rb / HALF : -1;
+    };
+    auto row_group = [&](int qt) { return split_block(qt) < 0 ? rb : rb % HALF; };
     const int qh = hg * G + slot;
     const int kvh = (hg * G) / p.group;
 
@@ -133,7 +154,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     auto issue_q = [&](int stage, int qt, int i) {
         const uint32_t qb = ring_base + stage * kStageBytes + wave * kQWaveBytes;
         const uint32_t lds[4] = {qb, qb + 1024, qb + 2048, qb + 3072};
-        const int base = (qt * BM + rb * 64 + i * 32) * q_row;
+        const int base = (qt * BM + row_group(qt) * 64 + i * 32) * q_row;
         const int off[4] = {base + qoff[0], base + qoff[1], base + qoff[2], base + qoff[3]};
         dma16x4(lds, off, q_rs, q_rs);
     };
@@ -194,7 +215,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
     bf16x8 qf[2][4];
     for (int qt = qt_first; qt < qt_end; ++qt) {
-        const int r0 = qt * BM + rb * 64;  // the wave's first row
+        const int kb_only = split_block(qt);  // >= 0 on every wave of a split tile
+        const int r0 = qt * BM + row_group(qt) * 64;  // the wave's first row
         const bool wave_active = r0 < L;
 
         // Q steps: half i of the wave's rows; the empty asm ends the reads' scope before the
@@ -287,15 +309,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             st0 = sum2(pb[1], 2, st0);
             st1 = sum2(pb[1], 3, st1);
         };
-        // The exact path, from half block `from` (2 b + x) of the stage's key tile to its end:
+        // The exact path, over half blocks [from, to) (2 b + x) of the stage's key tile:
         // scores recomputed from the stage (blocks past the keys skipped, the straddling block
         // masked), the maximum raised to cover them, probabilities, P.V. It serves the segment's
         // last, partial key tile (the first one too when the segment has fewer than 64 keys) and
         // the rest of a full tile whose stale-maximum softmax overflowed (whose earlier half
         // blocks are already added).
-        auto exact_from = [&](const __bf16 *kt, const __bf16 *vt, int kt0, int from) {
+        auto exact_from = [&](const __bf16 *kt, const __bf16 *vt, int kt0, int from, int to) {
 #pragma unroll 1
-            for (int hb = from; hb < 4; ++hb) {
+            for (int hb = from; hb < to; ++hb) {
                 const int b = hb >> 1, x = hb & 1;
                 const int kb0 = kt0 + 32 * b;
                 if (kb0 >= Lk) break;
@@ -419,25 +441,131 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             return 4;
         };
 
-        for (int t = 0; t < nkt; ++t) {
-            begin_step();
-            if (wave_active) {
-                const __bf16 *kt = &ring[stage][0][0];
-                const __bf16 *vt = &ring[stage][1][0];
-                const int kt0 = t * BN;
-                int from = 0;
-                if (kt0 + BN <= Lk) {
-                    // A query tile's first key tile seeds the stale maximum from its first
-                    // block's scores inside the pipelined schedule.
-                    from = pipelined_tile(t == 0, kt, vt);
-                }
-                if (from < 4) exact_from(kt, vt, kt0, from);
+        // One 32-key block b of a full key tile for both halves, the split tile's share of it,
+        // in the same pipelined order under the stale maximum (seeded from block b on the
+        // query tile's first key tile). Returns 4 when done, else the half block whose softmax
+        // overflowed.
+        auto pipelined_block = [&](bool first, const __bf16 *kt, const __bf16 *vt, int b) -> int {
+            bf16x8 k4[4], v4[2][2], pa[2], pbb[2];
+            float st0, st1;
+            load_k(kt, b, k4);
+            f32x16 sa = qk(k4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (first) seed_max(sa, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            f32x16 sb = qk(k4, 1);
+            probs(sa, 0, pa, st0, st1);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
             }
-            end_step();
+            __builtin_amdgcn_sched_barrier(0);
+            if (!accept(0, st0, st1)) return 2 * b;
+            if (first) seed_max(sb, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            load_v(vt, b, v4);
+            pv(v4, pa, 0);
+            probs(sb, 1, pbb, st0, st1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 9, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (!accept(1, st0, st1)) return 2 * b + 1;
+            __builtin_amdgcn_sched_barrier(0);
+            pv(v4, pbb, 1);
+            return 4;
+        };
+
+        if (kb_only < 0) {
+            for (int t = 0; t < nkt; ++t) {
+                begin_step();
+                if (wave_active) {
+                    const __bf16 *kt = &ring[stage][0][0];
+                    const __bf16 *vt = &ring[stage][1][0];
+                    const int kt0 = t * BN;
+                    int from = 0;
+                    if (kt0 + BN <= Lk) {
+                        // A query tile's first key tile seeds the stale maximum from its first
+                        // block's scores inside the pipelined schedule.
+                        from = pipelined_tile(t == 0, kt, vt);
+                    }
+                    if (from < 4) exact_from(kt, vt, kt0, from, 4);
+                }
+                end_step();
+            }
+        } else {
+            // A split tile: this wave's block of every key tile.
+            for (int t = 0; t < nkt; ++t) {
+                begin_step();
+                if (wave_active) {
+                    const __bf16 *kt = &ring[stage][0][0];
+                    const __bf16 *vt = &ring[stage][1][0];
+                    const int kt0 = t * BN;
+                    int from = 2 * kb_only;
+                    if (kt0 + BN <= Lk) from = pipelined_block(t == 0, kt, vt, kb_only);
+                    if (from < 2 * kb_only + 2) exact_from(kt, vt, kt0, from, 2 * kb_only + 2);
+                }
+                end_step();
+            }
+        }
+
+        // A split tile's halves meet: the helpers (second key block) hand their maxima, sums
+        // and accumulators to the primaries through LDS, half x at a time through the stage
+        // the last step read (no load is in flight to it until the next step begins, after
+        // a barrier). Every wave of the workgroup takes the branch and its barriers.
+        if (kb_only >= 0) {
+            float *xb = reinterpret_cast<float *>(&ring[stage == 0 ? NS - 1 : stage - 1][0][0]);
+            const int mg = slot * HALF + row_group(qt);  // the pair's merge buffer (< 2)
+            const bool helper = wave_active && kb_only == 1;
+            const bool primary = wave_active && kb_only == 0;
+            __syncthreads();
+            if (helper) {
+                merge_ml[mg][0][lane] = m[0];
+                merge_ml[mg][1][lane] = m[1];
+                merge_ml[mg][2][lane] = ls[0][0] + ls[0][1];
+                merge_ml[mg][3][lane] = ls[1][0] + ls[1][1];
+            }
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+                f32x4 *buf = reinterpret_cast<f32x4 *>(xb) + mg * 512;  // 8 KB per pair
+                if (helper) {
+#pragma unroll
+                    for (int db = 0; db < 2; ++db)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            buf[(db * 4 + c) * 64 + lane] = f32x4{o[x][db][4 * c], o[x][db][4 * c + 1],
+                                                                  o[x][db][4 * c + 2], o[x][db][4 * c + 3]};
+                }
+                __syncthreads();
+                if (primary) {
+                    const float mh = merge_ml[mg][x][lane], lh = merge_ml[mg][2 + x][lane];
+                    const float mn = fmaxf(m[x], mh);
+                    const float ap = m[x] > kNegInf ? exp2_fast(m[x] - mn) : 0.0f;
+                    const float ah = mh > kNegInf ? exp2_fast(mh - mn) : 0.0f;
+                    ls[x][0] = (ls[x][0] + ls[x][1]) * ap + lh * ah;
+                    ls[x][1] = 0.0f;
+#pragma unroll
+                    for (int db = 0; db < 2; ++db)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const f32x4 h = buf[(db * 4 + c) * 64 + lane];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) o[x][db][4 * c + e] = o[x][db][4 * c + e] * ap + h[e] * ah;
+                        }
+                }
+                if (x == 0) __syncthreads();
+            }
         }
 
         // Normalise, apply the gate, store both halves.
-        if (wave_active) {
+        if (wave_active && kb_only != 1) {
 #pragma unroll
             for (int x = 0; x < 2; ++x) {
                 const float lt = pair_sum(ls[x][0] + ls[x][1]);

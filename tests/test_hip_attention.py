@@ -155,6 +155,31 @@ def test_gqa_head_dims(pe, d, hq, hkv, causal):
     _assert_parity(got, want, cu)
 
 
+# Segments of more than 128 tokens whose last query tile holds rows for at most half of a
+# head's waves (1..128 rows past a multiple of 256 with one query head per workgroup, 1..64
+# past a multiple of 128 with two): the global kernel splits such a tile's key blocks between
+# two waves and merges their maxima, sums and accumulators. 257 and 321 leave the second wave
+# no key in the last key tile, 300 a masked partial block; the segments of at most 128 tokens
+# do not split.
+SPLIT_LENGTHS = [1, 20, 33, 64, 100, 128, 129, 160, 200, 257, 300, 321, 384, 385, 640, 700]
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (8, 2)], ids=["mha", "gqa2", "gqa4"])
+@pytest.mark.parametrize("gate", [False, True], ids=["plain", "gate"])
+def test_split_query_tiles_match_oracle(pe, hq, hkv, gate):
+    announce(f"split query tiles hq={hq} hkv={hkv} gate={gate}")
+    q, k, v, cu, gt = _inputs(SPLIT_LENGTHS, hq=hq, hkv=hkv, seed=53, gate=gate)
+    qd, kd, vd, cud, gd = _dev(q, k, v, cu, gt)
+    with torch.inference_mode():
+        got = pe.varlen_attention(qd, kd, vd, cud, max(SPLIT_LENGTHS), softmax_scale=0.125, gate=gd, short_max=0)
+        alone = [pe.varlen_attention(qd[a:b], kd[a:b], vd[a:b], cud.new_tensor([0, b - a]), b - a,
+                                     softmax_scale=0.125, gate=None if gd is None else gd[a:b], short_max=0)
+                 for a, b in zip(cu.tolist(), cu.tolist()[1:])]
+    _assert_parity(got, _oracle(q, k, v, cu, scale=0.125, gate=gt), cu)
+    # a tile splits by its segment's length alone: each segment's bits are its own
+    assert torch.equal(got, torch.cat(alone))
+
+
 @pytest.mark.parametrize("d,short_max", [(256, 0), (64, 64), (128, 32)])
 def test_fused_sigmoid_gate(pe, d, short_max):
     lengths = [16, 300, 40, 129]
