@@ -4,9 +4,13 @@
 // tiled_attn_kernel (pe_attn_tiled.h), with a step loop shaped for the register budget of
 // wide heads, whose O accumulators alone take D / 2 VGPRs per lane: one copy of the step (the
 // ring stage is a register), the exact running maximum of every tile (lazy rescale above 2^8),
-// fp32 sums of the unrounded probabilities (the reference's precision strategy,
-// packed_encoders/_kernels/triton_packed_attention.py:122-136), and loads issued only for real
-// steps, the wait count following how many are in flight.
+// and loads issued only for real steps, the wait count following how many are in flight. The
+// row sums add the bf16-rounded probabilities the P.V product uses (v_dot2 with ones), as the
+// head_dim 64 kernels do: under the lazily raised maximum a row's dominant probability is not
+// exactly 1, and summing it unrounded would leave its bf16 rounding (up to 2^-9 relative) in
+// the output. (The reference sums the unrounded values,
+// packed_encoders/_kernels/triton_packed_attention.py:122-136, with a maximum that is exact per
+// block.)
 #pragma once
 
 #include "pe_attn_tiled.h"
@@ -299,14 +303,12 @@ __global__ __launch_bounds__(256) void wide_attn_kernel(AttnParams p) {
             for (int b = 0; b < NB; ++b) {
                 if (live[b]) {
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) {
-                        const float e = exp2_fast(fmaf(s[b][j], c2, -muse));
-                        s[b][j] = e;
-                        ls[j & 3] += e;
-                    }
+                    for (int j = 0; j < 16; ++j) s[b][j] = exp2_fast(fmaf(s[b][j], c2, -muse));
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         const bf16x8 pb = to_bf16x8(s[b], 8 * h);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) ls[i] = sum2(pb, i, ls[i]);
 #pragma unroll
                         for (int db = 0; db < DB; ++db) {
                             const bf16x4 lo = tr16(vt + (32 * b + 16 * h) * D + vbase[0][db]);

@@ -318,11 +318,10 @@ __global__ __launch_bounds__(64 * NW) void wide16_attn_kernel(AttnParams p) {
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float e = exp2_fast(fmaf(s[kb][i], c2, -muse));
-                        ls[i] += e;
-                        pb[4 * kb + i] = (__bf16)e;
-                    }
+                    for (int i = 0; i < 4; ++i) pb[4 * kb + i] = (__bf16)exp2_fast(fmaf(s[kb][i], c2, -muse));
+                // row sums of the rounded probabilities, the values the P.V product weighs
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ls[i] = sum2(pb, i, ls[i]);
 #pragma unroll
                 for (int db = 0; db < DB; ++db) {
                     const __bf16 *va = vt + 128 * (db >> 3) + vaddr[db & 7];

@@ -1,0 +1,127 @@
+"""Seeded random calls over the whole argument space of varlen_attention against the oracle.
+
+The other GPU tests pin each feature on chosen shapes; these cases draw the features together,
+as a caller combines them: head_dim 64 / 128 / 256, MHA and GQA, global, +-64, asymmetric and
+one-sided windows, causal with and without a left window, the sigmoid gate, separate key
+segments (longer, equal or shorter than their queries), empty segments, every routing boundary,
+a host lower bound on the lengths, the band kernel forced on or off, and logits at 1x and 2x
+N(0,1). Each case is a pure function of its seed (numpy's PCG64), so a failure names a
+reproducible call. Bar: the reference's tolerances (max-abs 2e-2, per-token cosine 0.9999).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import attention as oa
+
+MAX_ABS = 2e-2
+MIN_COS = 0.9999
+HEADS = [(4, 4), (8, 2), (6, 3), (8, 8), (4, 1), (12, 12)]
+N_CASES = 96
+
+
+def _lengths(rng, kind: str) -> list[int]:
+    n = int(rng.integers(1, 20))
+    if kind == "short":
+        out = rng.integers(0, 65, size=n)
+    elif kind == "mixed":
+        out = np.where(rng.random(n) < 0.6, rng.integers(0, 129, size=n), rng.integers(129, 701, size=n))
+    else:
+        out = rng.integers(200, 901, size=max(1, n // 3))
+    out = [int(x) for x in out]
+    if max(out) == 0:
+        out[0] = 1
+    return out
+
+
+def draw_case(seed: int) -> dict:
+    """The call of case `seed`: every argument of varlen_attention and the inputs' shapes."""
+    rng = np.random.default_rng(seed)
+    d = int(rng.choice([64, 64, 64, 128, 256]))
+    hq, hkv = HEADS[int(rng.integers(len(HEADS)))]
+    if d == 256:
+        hq, hkv = min(hq, 8), min(hkv, 8)
+        hq -= hq % hkv
+    lengths = _lengths(rng, str(rng.choice(["short", "mixed", "long"])))
+    causal = bool(rng.random() < 0.3)
+    kind = str(rng.choice(["global", "band64", "asym", "one-sided"], p=[0.3, 0.4, 0.15, 0.15]))
+    if kind == "global":
+        window = (-1, -1)
+    elif kind == "band64":
+        window = (64, 64)
+    elif kind == "asym":
+        window = (int(rng.integers(0, 200)), int(rng.integers(0, 200)))
+    else:
+        window = (int(rng.integers(0, 300)), -1) if rng.random() < 0.5 else (-1, int(rng.integers(0, 300)))
+    if causal:
+        window = (window[0], -1)
+    keys = None
+    if rng.random() < 0.2:
+        keys = [max(0, n + int(rng.integers(-20, 200))) for n in lengths]
+        keys[0] = max(keys[0], 1)
+    short_max = [None, 0, 32, 64, 128][int(rng.integers(5))] if d <= 128 else [None, 0][int(rng.integers(2))]
+    band_kernel = int(rng.integers(3))  # calls the band kernel cannot serve ignore it
+    if seed % 8 == 7:  # every eighth case a shape the streaming band kernel serves
+        d, window, causal, keys = 64, (64, 64), False, None
+        hq, hkv = [(4, 4), (12, 12), (6, 2)][int(rng.integers(3))]
+    return {"seed": seed, "d": d, "hq": hq, "hkv": hkv, "lengths": lengths, "keys": keys,
+            "window": window, "causal": causal, "gate": bool(rng.random() < 0.3), "short_max": short_max,
+            "band_kernel": band_kernel, "bound": bool(rng.random() < 0.3),
+            "logit_scale": float(rng.choice([1.0, 1.0, 2.0]))}
+
+
+def test_draws_cover_the_argument_space():
+    """The drawn cases reach every head dim, window kind, causal, the gate, separate keys, empty
+    segments, every routing boundary and the forced band kernel (a CPU check of the generator,
+    so the GPU cases below cannot silently narrow)."""
+    cases = [draw_case(s) for s in range(N_CASES)]
+    assert {c["d"] for c in cases} == {64, 128, 256}
+    assert {c["window"] == (-1, -1) for c in cases} == {True, False}
+    assert any(c["window"] == (64, 64) for c in cases)
+    assert any(c["causal"] for c in cases) and any(c["gate"] for c in cases)
+    assert any(c["keys"] is not None for c in cases)
+    assert any(0 in c["lengths"] for c in cases)
+    assert {c["short_max"] for c in cases} == {None, 0, 32, 64, 128}
+    assert any(c["hq"] != c["hkv"] for c in cases)
+    band = [c for c in cases if c["d"] == 64 and c["window"] == (64, 64) and not c["causal"]
+            and c["keys"] is None and (c["hq"] // c["hkv"]) % 2 == 1]  # shapes the band kernel serves
+    assert {c["band_kernel"] for c in band} == {0, 1, 2}
+    assert any(c["bound"] for c in cases) and any(c["logit_scale"] == 2.0 for c in cases)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(N_CASES))
+def test_random_call_matches_oracle(pe, seed):
+    c = draw_case(seed)
+    announce(f"random case {c}")
+    g = torch.Generator().manual_seed(1000 + seed)
+    lengths, keys = c["lengths"], c["keys"] if c["keys"] is not None else c["lengths"]
+    T, Tk = sum(lengths), sum(keys)
+    q = (torch.randn(T, c["hq"], c["d"], generator=g) * c["logit_scale"]).bfloat16()
+    k = (torch.randn(Tk, c["hkv"], c["d"], generator=g) * c["logit_scale"]).bfloat16()
+    v = torch.randn(Tk, c["hkv"], c["d"], generator=g).bfloat16()
+    gt = torch.randn(T, c["hq"], c["d"], generator=g).bfloat16() if c["gate"] else None
+    cu = torch.tensor([0, *np.cumsum(lengths).tolist()], dtype=torch.int32)
+    cuk = torch.tensor([0, *np.cumsum(keys).tolist()], dtype=torch.int32) if c["keys"] is not None else None
+    scale = c["d"] ** -0.5
+    with torch.inference_mode():
+        got = pe.varlen_attention(
+            q.cuda(), k.cuda(), v.cuda(), cu.cuda(), max(lengths), softmax_scale=scale, window=c["window"],
+            causal=c["causal"], gate=None if gt is None else gt.cuda(), short_max=c["short_max"],
+            cu_seqlens_k=None if cuk is None else cuk.cuda(), max_seqlen_k=max(keys) if cuk is not None else None,
+            band_kernel=c["band_kernel"], min_seqlen=min(lengths) if c["bound"] else None)
+    f = lambda t: t.float().numpy()
+    want = oa.packed_attention(f(q), f(k), f(v), cu.numpy(), scale=scale, window=c["window"], causal=c["causal"],
+                               gate=None if gt is None else f(gt), cu_seqlens_k=None if cuk is None else cuk.numpy())
+    got = got.float().cpu().numpy().astype(np.float64)
+    assert np.isfinite(got[:T]).all()
+    err = np.abs(got[:T] - want[:T])
+    assert err.max() <= MAX_ABS, f"case {seed}: max abs {err.max():.4g}"
+    zero = ~np.any(want[:T].reshape(T, -1), axis=1)  # rows that reach no key
+    assert not np.any(got[:T].reshape(T, -1)[zero]), f"case {seed}: rows that reach no key must be zero"
+    cos = oa.cosine_per_token(got[:T][~zero], want[:T][~zero])
+    assert cos.size == 0 or cos.min() >= MIN_COS, f"case {seed}: min cosine {cos.min():.6f}"
