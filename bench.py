@@ -1056,6 +1056,88 @@ def compare_libraries(args, paths: list[str]) -> int:
     return 0
 
 
+def variant_timing(args, which: str) -> int:
+    """Interleaved medians of one layer call of ``--workload`` in two forms, on the in-tree
+    library: ``gate`` the call with and without its sigmoid gate (what the fused gate costs);
+    ``side-stream`` a mixed batch's short pass on a second stream (default priority) beside the
+    plan and the long-segment kernel, joined before the call ends, against the library's
+    one-stream order (outputs checked bit for bit). ``--samples`` rounds of ``--steps`` calls,
+    cycling over four Q/K/V sets."""
+    import torch
+
+    from packed_encoders_amd import _lib, hip_attention as hip
+    from packed_encoders_amd.attention_dispatch import hip_short_max
+
+    workload = WORKLOADS[args.workload]()
+    layer = workload.layers[0]
+    dev = torch.device("cuda", 0)
+    T, hq, hkv, d = workload.total_tokens, workload.n_heads_q, workload.n_heads_kv, workload.head_dim
+    gen = torch.Generator(device=dev).manual_seed(1)
+    sets = []
+    for _ in range(4):
+        q, k, v = (torch.randn(T, h, d, device=dev, generator=gen, dtype=torch.bfloat16) for h in (hq, hkv, hkv))
+        sets.append((q, k, v, torch.randn(T, hq, d, device=dev, generator=gen, dtype=torch.bfloat16)))
+    cu = torch.tensor(workload.cu_seqlens(), dtype=torch.int32, device=dev)
+    lib = _lib.library()
+    short_max = hip_short_max(d, max_seqlen=workload.max_seqlen) if args.short_max is None else args.short_max
+    outs = [torch.zeros(T, hq, d, device=dev, dtype=torch.bfloat16) for _ in sets]
+
+    def arglist(gate: bool, bound: int):
+        return [hip._args(q, k, v, o, cu, workload.max_seqlen, workload.scale, layer.window[0], layer.window[1],
+                          layer.causal, g if gate else None, short_max, args.strip, min_seqlen=bound)
+                for (q, k, v, g), o in zip(sets, outs)]
+
+    main = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(dev)
+    counter = [0]
+    if which == "gate":
+        if not layer.gate:
+            raise SystemExit(f"{workload.name}'s layer has no gate")
+        forms = {"gate": arglist(True, min(workload.lengths)), "no_gate": arglist(False, min(workload.lengths))}
+    else:
+        forms = {"one_stream": arglist(layer.gate, 0), "side_stream": arglist(layer.gate, 0)}
+    size = ctypes.c_size_t()
+    assert lib.pe_attn_workspace_size(ctypes.byref(next(iter(forms.values()))[0]), ctypes.byref(size)) == 0
+    ws = torch.zeros(max(1, size.value), dtype=torch.uint8, device=dev)
+
+    def call(form: str):
+        a = ctypes.byref(forms[form][counter[0] % len(sets)])
+        counter[0] += 1
+        s = main.cuda_stream
+        if form == "side_stream":
+            side.wait_stream(main)
+            assert lib.pe_attn_short_fwd(a, side.cuda_stream) == 0
+        elif which != "gate":
+            assert lib.pe_attn_short_fwd(a, s) == 0
+        if which != "gate" or counter[0] <= len(sets):
+            assert lib.pe_attn_plan(a, ws.data_ptr(), size.value, s) == 0
+        assert lib.pe_attn_tiled_fwd(a, ws.data_ptr(), size.value, s) == 0
+        if form == "side_stream":
+            main.wait_stream(side)
+
+    check = {}
+    for form in forms:
+        for _ in sets:
+            call(form)
+        torch.cuda.synchronize()
+        check[form] = [o.clone() for o in outs]
+    same = None if which == "gate" else all(torch.equal(a, b) for a, b in zip(*check.values()))
+    settle(lambda: [call(f) for f in forms], args.settle)
+    res = {f: [] for f in forms}
+    for _ in range(args.samples):
+        for form in forms:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                call(form)
+            e1.record()
+            torch.cuda.synchronize()
+            res[form].append(round(e0.elapsed_time(e1) * 1e3 / args.steps, 2))
+    print(json.dumps({"variant_timing": which, "workload": workload.name, "bit_identical": same,
+                      **{f: {"median_us": statistics.median(v), "us": v} for f, v in res.items()}}), flush=True)
+    return 0
+
+
 def dispatch_sweep(reps: int = 20, replays: int = 5) -> int:
     """Short kernel vs tiled kernel per segment length: the measurement the gfx950 routing
     boundary (attention_dispatch.HipDispatchPolicy) is fitted to. For head_dim 64 (12 heads)
@@ -1149,6 +1231,9 @@ def main() -> int:
     ap.add_argument("--window", choices=("global", "band"), default=None,
                     help="--compare: the layer's window (default: the workload's first layer)")
     ap.add_argument("--sets", type=int, default=4, help="--compare: distinct Q/K/V sets cycled over (default 4)")
+    ap.add_argument("--variant-timing", choices=("gate", "side-stream"), default=None,
+                    help="only time one layer call of --workload in two forms, interleaved: with and without its "
+                         "gate, or a mixed batch's short pass on a second stream against one stream")
     ap.add_argument("--graph-overhead", action="store_true",
                     help="only measure a HIP-graph replay's fixed and per-node cost against eager launches")
     ap.add_argument("--peaks", action="store_true",
@@ -1183,6 +1268,8 @@ def main() -> int:
         return graph_overhead()
     if args.compare:
         return compare_libraries(args, args.compare)
+    if args.variant_timing:
+        return variant_timing(args, args.variant_timing)
 
     import packed_encoders_amd as pe
 
