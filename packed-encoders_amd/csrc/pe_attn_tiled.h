@@ -308,7 +308,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
                 // Every block of the tile live and unmasked for all of this wave's rows: the
                 // common case, taken without any per-block test.
                 const bool full = (kt0 + BN <= Lk) && (wl < 0 || (a1 - 1) - kt0 <= wl) && (wr < 0 || (kt0 + BN - 1) - a0 <= wr);
-                // (Kept as a lambda: the register allocator then fits the step in 136-148 VGPRs;
+                // (Kept as a lambda: the register allocator then fits the kernel in 160-164 VGPRs;
                 // written inline the same code spills.)
                 auto kv_step = [&]() {
                     bool live[NB];
