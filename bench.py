@@ -453,11 +453,21 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+# FLOPs the CPU leg's timed step may take (the whole schedule up to this, else whole segments
+# from the front of the batch), and the 1-thread run's sample: about 1 s and 1-3 s of CPU work
+# per repeat on the GPU boxes' 16 threads, so the default run stays within minutes.
+CPU_STEP_FLOPS = 1.0e12
+CPU_ONE_THREAD_FLOPS = 1.0e11
+
+
 def cpu_bench(workload, repeats: int = 7):
     """The same attention schedule on the host CPU (fp32): one warm-up, then the median of
     ``repeats`` timed steps on all physical cores (benchmarks/cpu/README.md:27-31), and a
     1-thread run on a bounded sample (the first global and the first banded layer, median of
-    3) scaled to the same unit."""
+    3) scaled to the same unit. A schedule past CPU_STEP_FLOPS (C4's global layer: 4.4e12) is
+    timed on the whole segments at the front of the batch that fit it, the 1-thread run on
+    those that fit CPU_ONE_THREAD_FLOPS (at least one); TFLOP/s is a rate, so a sample of whole
+    segments measures it without scaling."""
     import numpy as np
     import torch
     import torch.nn.functional as F
@@ -472,12 +482,31 @@ def cpu_bench(workload, repeats: int = 7):
     if workload.n_heads_kv != hq:
         return None
     gen = torch.Generator().manual_seed(99)
-    q, k, v = (torch.randn(hq, T, d, generator=gen) for _ in range(3))
-    qn, kn, vn = (t.numpy() for t in (q, k, v))
-    out = np.empty((hq, T, d), dtype=np.float32)
-    lengths = list(workload.lengths)
-    longest = max(lengths)
-    offsets = np.concatenate([[0], np.cumsum(lengths)])
+    q_all, k_all, v_all = (torch.randn(hq, T, d, generator=gen) for _ in range(3))
+    all_lengths = list(workload.lengths)
+
+    def front(layers, cap: float) -> int:
+        """Whole segments from the front of the batch whose FLOPs over `layers` fit `cap`."""
+        n, acc = 0, 0.0
+        for length in all_lengths:
+            f = sum(hip.useful_flops([length], hq, d, window=l.window) for l in layers)
+            if n and acc + f > cap:
+                break
+            n, acc = n + 1, acc + f
+        return n
+
+    q = k = v = qn = kn = vn = out = lengths = longest = offsets = None
+
+    def use(n_seg: int):
+        """Time the first n_seg segments from here on (contiguous fp32 copies of their rows)."""
+        nonlocal q, k, v, qn, kn, vn, out, lengths, longest, offsets
+        lengths = all_lengths[:n_seg]
+        t = sum(lengths)
+        q, k, v = (x[:, :t].contiguous() for x in (q_all, k_all, v_all))
+        qn, kn, vn = (x.numpy() for x in (q, k, v))
+        out = np.empty((hq, t, d), dtype=np.float32)
+        longest = max(lengths)
+        offsets = np.concatenate([[0], np.cumsum(lengths)])
 
     def layer_call(layer, n_threads):
         if layer.causal or layer.gate or layer.window[0] != layer.window[1]:
@@ -506,22 +535,31 @@ def cpu_bench(workload, repeats: int = 7):
             times.append(time.perf_counter() - t0)
         return statistics.median(times)
 
+    n_step = front(workload.layers, CPU_STEP_FLOPS)
+    use(n_step)
     seconds = timed(workload.layers, threads, repeats)
     flops = sum(hip.useful_flops(lengths, hq, d, window=l.window) for l in workload.layers)
-    # 1 thread: one layer of each kind present, scaled by its share of the schedule's FLOPs
+    step_t = sum(lengths)
+    # 1 thread: one layer of each kind present, on the segments that fit its cap
     kinds = []
     for layer in workload.layers:
         if layer not in kinds:
             kinds.append(layer)
+    n_one = min(n_step, front(kinds, CPU_ONE_THREAD_FLOPS))
+    use(n_one)
     one_flops = sum(hip.useful_flops(lengths, hq, d, window=l.window) for l in kinds)
     one_seconds = timed(kinds, 1, 3)
     one_tflops = one_flops / one_seconds / 1e12
     model = cpu_model()
-    sample = (f"full {workload.name} schedule ({len(workload.layers)} attention layers, T={T}) in fp32 on {threads} "
-              f"threads (physical cores of the affinity mask), median of {repeats} after 1 warm-up; band/short "
-              f"layers: {'reference pe_local_attention (oracle/_ref)' if kind == 'reference' else 'oracle C port'}; "
+    whole = n_step == len(all_lengths)
+    what = (f"full {workload.name} schedule ({len(workload.layers)} attention layers, T={T})" if whole else
+            f"{workload.name} schedule ({len(workload.layers)} attention layers) on its first {n_step} of "
+            f"{len(all_lengths)} segments (T={step_t} of {T}, {flops:.3g} of the step's FLOPs)")
+    sample = (f"{what} in fp32 on {threads} threads (physical cores of the affinity mask), median of {repeats} "
+              f"after 1 warm-up; band/short layers: "
+              f"{'reference pe_local_attention (oracle/_ref)' if kind == 'reference' else 'oracle C port'}; "
               f"global layers longer than 128: per-segment torch SDPA. 1-thread: one layer of each kind "
-              f"({len(kinds)}), median of 3")
+              f"({len(kinds)}) on the first {n_one} segment(s), median of 3")
     log(f"cpu baseline ({kind}, {threads} threads, {model}): {seconds * 1e3:.1f} ms/step -> "
         f"{flops / seconds / 1e12:.3f} TFLOP/s; 1 thread {one_tflops:.4f} TFLOP/s")
     return {"value": round(flops / seconds / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": kind,

@@ -93,3 +93,25 @@ def test_port_rejects_bad_arguments():
 
 def test_physical_cores_positive():
     assert cpu.physical_cores() >= 1
+
+
+def test_cpu_leg_samples_whole_segments_past_its_flop_cap(monkeypatch):
+    """bench.cpu_bench on a schedule past its caps times the whole segments at the front of the
+    batch that fit them (at least one), says so in its sample, and reports the sample's own
+    FLOP rate; under the caps it keeps the full schedule."""
+    import bench
+    from packed_encoders_amd import hip_attention as hip
+    from packed_encoders_amd.workloads import GLOBAL, Workload
+
+    lengths = (40, 60, 50, 30)
+    w = Workload("T4", lengths, 2, 2, 64, (GLOBAL,), "four short documents")
+    per_seg = [hip.useful_flops([n], 2, 64, window=(-1, -1)) for n in lengths]
+    monkeypatch.setattr(bench, "CPU_STEP_FLOPS", per_seg[0] + per_seg[1] + 1)
+    monkeypatch.setattr(bench, "CPU_ONE_THREAD_FLOPS", 1.0)
+    r = bench.cpu_bench(w, repeats=1)
+    assert "first 2 of 4 segments" in r["sample"] and "on the first 1 segment(s)" in r["sample"]
+    assert r["value"] > 0 and r["one_thread"]["value"] > 0
+    monkeypatch.setattr(bench, "CPU_STEP_FLOPS", 1e15)
+    monkeypatch.setattr(bench, "CPU_ONE_THREAD_FLOPS", 1e15)
+    r = bench.cpu_bench(w, repeats=1)
+    assert r["sample"].startswith("full T4 schedule") and "on the first 4 segment(s)" in r["sample"]
