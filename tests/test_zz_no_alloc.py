@@ -64,6 +64,52 @@ def test_noalloc_matches_workspace_entry_point_on_two_calls(pe, d, hq, hkv, wind
         assert torch.equal(got, want), f"call {call}: noalloc output differs from the workspace entry point"
 
 
+def test_noalloc_matches_workspace_entry_point_on_random_calls(pe):
+    """The first 24 seeded calls of the random parity sweep (tests/test_random_gpu.py: every
+    head dim, windows, causal, the gate, separate key segments, routing boundaries, host length
+    bounds, forced band kernels), one after another on one device: the no-allocation entry point
+    gives the workspace entry point's bits on each, whatever the previous call left in the
+    static array."""
+    from test_random_gpu import draw_case
+
+    from packed_encoders_amd import _lib
+    from packed_encoders_amd.hip_attention import _args
+
+    lib = _lib.library()
+    stream = torch.cuda.current_stream().cuda_stream
+    for seed in range(24):
+        c = draw_case(seed)
+        announce(f"noalloc random case {seed}: d={c['d']} heads={c['hq']}/{c['hkv']} window={c['window']} "
+                 f"causal={c['causal']} keys={c['keys'] is not None}")
+        g = torch.Generator().manual_seed(500 + seed)
+        lengths = c["lengths"]
+        keys = c["keys"] if c["keys"] is not None else lengths
+        T, Tk = sum(lengths), sum(keys)
+        q = torch.randn(T, c["hq"], c["d"], generator=g).bfloat16().cuda()
+        k = torch.randn(Tk, c["hkv"], c["d"], generator=g).bfloat16().cuda()
+        v = torch.randn(Tk, c["hkv"], c["d"], generator=g).bfloat16().cuda()
+        gt = torch.randn(T, c["hq"], c["d"], generator=g).bfloat16().cuda() if c["gate"] else None
+        cu = torch.tensor([0, *np.cumsum(lengths).tolist()], dtype=torch.int32, device="cuda")
+        cuk = (torch.tensor([0, *np.cumsum(keys).tolist()], dtype=torch.int32, device="cuda")
+               if c["keys"] is not None else None)
+        outs = []
+        for fn in ("workspace", "noalloc"):
+            out = torch.full(q.shape, 5.0, dtype=torch.bfloat16, device="cuda")
+            a = _args(q, k, v, out, cu, max(lengths), c["d"] ** -0.5, c["window"][0], c["window"][1], c["causal"], gt,
+                      -1 if c["short_max"] is None else c["short_max"], 0, cuk, max(keys) if cuk is not None else 0,
+                      c["band_kernel"], min(lengths) if c["bound"] else 0)
+            if fn == "noalloc":
+                assert lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(a), stream) == 0
+            else:
+                size = ctypes.c_size_t()
+                assert lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size)) == 0
+                ws = torch.empty(max(size.value, 1), dtype=torch.uint8, device="cuda")
+                assert lib.pe_varlen_attn_fwd(ctypes.byref(a), ws.data_ptr(), size.value, stream) == 0
+            torch.cuda.synchronize()
+            outs.append(out[:T])
+        assert torch.equal(outs[0], outs[1]), f"random case {seed}: noalloc output differs from the workspace entry point"
+
+
 def _inputs(T, hq, hkv, d, seed):
     g = torch.Generator().manual_seed(seed)
     return [torch.randn(T, h, d, generator=g).bfloat16().cuda() for h in (hq, hkv, hkv)]
