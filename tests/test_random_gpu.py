@@ -4,8 +4,8 @@ The other GPU tests pin each feature on chosen shapes; these cases draw the feat
 as a caller combines them: head_dim 64 / 128 / 256, MHA and GQA, global, +-64, asymmetric and
 one-sided windows, causal with and without a left window, the sigmoid gate, separate key
 segments (longer, equal or shorter than their queries), empty segments, every routing boundary,
-a host lower bound on the lengths, the band kernel forced on or off, and logits at 1x, 2x and 4x
-N(0,1). Each case is a pure function of its seed (numpy's PCG64), so a failure names a
+a host lower bound on the lengths, the band kernel forced on or off, logits at 1x, 2x and 4x
+N(0,1), and contiguous tensors or strided views into packed projection rows. Each case is a pure function of its seed (numpy's PCG64), so a failure names a
 reproducible call. Bar: the reference's tolerances (max-abs 2e-2, per-token cosine 0.9999),
 except where 2e-2 is less than the output's own rounding step: an output of magnitude 2 or
 more (peaked rows at 2x and 4x logits) has a bf16 step of 2^-6 and above, and a kernel output a
@@ -97,7 +97,36 @@ def draw_case(seed: int) -> dict:
     return {"seed": seed, "d": d, "hq": hq, "hkv": hkv, "lengths": lengths, "keys": keys,
             "window": window, "causal": causal, "gate": bool(rng.random() < 0.3), "short_max": short_max,
             "band_kernel": band_kernel, "bound": bool(rng.random() < 0.3),
-            "logit_scale": float(rng.choice([1.0, 1.0, 2.0, 4.0]))}
+            "logit_scale": float(rng.choice([1.0, 1.0, 2.0, 4.0])),
+            "packed": bool(rng.random() < 0.35)}
+
+
+def _device_inputs(c, q, k, v, gt):
+    """The call's device tensors: contiguous copies, or (c["packed"]) strided views into packed
+    projection rows, as callers hand them over: per head [q | gate] interleaved when there is
+    a gate (packed_encoders/arch/qwen3_5/engine.py:556-558: head stride 2 d), then k and v in
+    the same rows (keys shared with the queries) or in packed rows of their own, each row
+    padded by 64 elements."""
+    if not c["packed"]:
+        return [None if t is None else t.cuda() for t in (q, k, v, gt)]
+    T, hq, d = q.shape
+    Tk, hkv = k.shape[0], k.shape[1]
+    qg = torch.stack([q, gt], dim=2).reshape(T, hq * 2 * d) if gt is not None else q.reshape(T, hq * d)
+    kv = torch.cat([k.reshape(Tk, hkv * d), v.reshape(Tk, hkv * d)], dim=1)
+    if c["keys"] is None:
+        rows = torch.cat([qg, kv, torch.zeros(T, 64, dtype=q.dtype)], dim=1).cuda()
+        qg_d, kv_d = rows[:, :qg.shape[1]], rows[:, qg.shape[1]:qg.shape[1] + kv.shape[1]]
+    else:
+        qg_d = torch.cat([qg, torch.zeros(T, 64, dtype=q.dtype)], dim=1).cuda()[:, :qg.shape[1]]
+        kv_d = torch.cat([kv, torch.zeros(Tk, 64, dtype=q.dtype)], dim=1).cuda()[:, :kv.shape[1]]
+    if gt is not None:
+        heads = qg_d.view(T, hq, 2 * d)
+        qd, gd = heads[..., :d], heads[..., d:]
+    else:
+        qd, gd = qg_d.view(T, hq, d), None
+    kd = kv_d[:, :hkv * d].view(Tk, hkv, d)
+    vd = kv_d[:, hkv * d:].view(Tk, hkv, d)
+    return qd, kd, vd, gd
 
 
 def test_draws_cover_the_argument_space():
@@ -117,6 +146,8 @@ def test_draws_cover_the_argument_space():
             and c["keys"] is None and (c["hq"] // c["hkv"]) % 2 == 1]  # shapes the band kernel serves
     assert {c["band_kernel"] for c in band} == {0, 1, 2}
     assert any(c["bound"] for c in cases) and {c["logit_scale"] for c in cases} == {1.0, 2.0, 4.0}
+    assert {(c["packed"], c["gate"]) for c in cases} == {(False, False), (False, True), (True, False), (True, True)}
+    assert any(c["packed"] and c["keys"] is not None for c in cases)
 
 
 @pytest.mark.gpu
@@ -134,10 +165,13 @@ def test_random_call_matches_oracle(pe, seed):
     cu = torch.tensor([0, *np.cumsum(lengths).tolist()], dtype=torch.int32)
     cuk = torch.tensor([0, *np.cumsum(keys).tolist()], dtype=torch.int32) if c["keys"] is not None else None
     scale = c["d"] ** -0.5
+    qd, kd, vd, gd = _device_inputs(c, q, k, v, gt)
+    if c["packed"]:
+        assert not qd.is_contiguous() and not kd.is_contiguous()
     with torch.inference_mode():
         got = pe.varlen_attention(
-            q.cuda(), k.cuda(), v.cuda(), cu.cuda(), max(lengths), softmax_scale=scale, window=c["window"],
-            causal=c["causal"], gate=None if gt is None else gt.cuda(), short_max=c["short_max"],
+            qd, kd, vd, cu.cuda(), max(lengths), softmax_scale=scale, window=c["window"],
+            causal=c["causal"], gate=gd, short_max=c["short_max"],
             cu_seqlens_k=None if cuk is None else cuk.cuda(), max_seqlen_k=max(keys) if cuk is not None else None,
             band_kernel=c["band_kernel"], min_seqlen=min(lengths) if c["bound"] else None)
     f = lambda t: t.float().numpy()
