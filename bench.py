@@ -1107,6 +1107,8 @@ def variant_timing(args, which: str) -> int:
     from packed_encoders_amd.attention_dispatch import hip_short_max
 
     workload = WORKLOADS[args.workload]()
+    if which == "rope":
+        return _rope_timing(args, workload)
     layer = workload.layers[0]
     dev = torch.device("cuda", 0)
     T, hq, hkv, d = workload.total_tokens, workload.n_heads_q, workload.n_heads_kv, workload.head_dim
@@ -1173,6 +1175,75 @@ def variant_timing(args, which: str) -> int:
             res[form].append(round(e0.elapsed_time(e1) * 1e3 / args.steps, 2))
     print(json.dumps({"variant_timing": which, "workload": workload.name, "bit_identical": same,
                       **{f: {"median_us": statistics.median(v), "us": v} for f, v in res.items()}}), flush=True)
+    return 0
+
+
+def _rope_timing(args, workload) -> int:
+    """``--variant-timing rope``: RoPE + attention of one layer of an all-short workload (Q4096,
+    C1) from the packed projection ``qkv [T, 3*H*D]`` with per-token tables, in two forms,
+    interleaved: the RoPE kernel writing q and k then the attention call, and the attention call
+    with the RoPE fused into its prologue (``varlen_attention(rope=...)``). Outputs are checked
+    bit for bit; compulsory bytes of each form are reported beside the times."""
+    import torch
+
+    from packed_encoders_amd import ops
+    from packed_encoders_amd.hip_attention import rope_qkv, varlen_attention
+
+    layer = workload.layers[0]
+    dev = torch.device("cuda", 0)
+    T, h, d = workload.total_tokens, workload.n_heads_q, workload.head_dim
+    if workload.n_heads_kv != h or not ops.fused_rope_applies(torch.empty(1, dtype=torch.bfloat16, device=dev),
+                                                              d, workload.max_seqlen):
+        raise SystemExit(f"{workload.name}: the fused RoPE serves all-short MHA calls (head_dim 64/128, <= 128 tokens)")
+    gen = torch.Generator(device=dev).manual_seed(3)
+    cu = torch.tensor(workload.cu_seqlens(), dtype=torch.int32, device=dev)
+    theta = torch.arange(0, d, 2, device=dev, dtype=torch.float32) / d
+    pos = torch.cat([torch.arange(n, device=dev) for n in workload.lengths]).float()
+    ang = pos[:, None] * (10000.0 ** -theta)[None]
+    cos = torch.cat([ang.cos(), ang.cos()], dim=1).bfloat16()
+    sin = torch.cat([ang.sin(), ang.sin()], dim=1).bfloat16()
+    sets = [torch.randn(T, 3 * h * d, device=dev, generator=gen, dtype=torch.bfloat16) for _ in range(4)]
+    counter = [0]
+    kw = dict(softmax_scale=workload.scale, window=layer.window)
+
+    def two_steps():
+        qkv = sets[counter[0] % 4]
+        counter[0] += 1
+        q, k = rope_qkv(qkv, h, d, cos, sin)
+        return varlen_attention(q, k, qkv.view(T, 3, h, d)[:, 2], cu, workload.max_seqlen, **kw)
+
+    def fused():
+        qkv = sets[counter[0] % 4]
+        counter[0] += 1
+        view = qkv.view(T, 3, h, d)
+        return varlen_attention(view[:, 0], view[:, 1], view[:, 2], cu, workload.max_seqlen, rope=(cos, sin), **kw)
+
+    forms = {"rope_then_attention": two_steps, "fused": fused}
+    with torch.inference_mode():
+        outs = {}
+        for name, f in forms.items():
+            counter[0] = 0
+            outs[name] = f()
+        torch.cuda.synchronize()
+        same = torch.equal(*outs.values())
+        settle(lambda: [f() for f in forms.values()], args.settle)
+        res = {f: [] for f in forms}
+        for _ in range(args.samples):
+            for name, f in forms.items():
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(args.steps):
+                    f()
+                e1.record()
+                torch.cuda.synchronize()
+                res[name].append(round(e0.elapsed_time(e1) * 1e3 / args.steps, 2))
+    row = 2 * h * d  # bytes of one head-row set of one tensor per token
+    table = 2 * 2 * d  # cos and sin rows per token
+    moved = {"rope_then_attention": T * (2 * row + 2 * row + table) + T * (3 * row + row),
+             "fused": T * (3 * row + row + table)}
+    print(json.dumps({"variant_timing": "rope", "workload": workload.name, "bit_identical": same,
+                      **{f: {"median_us": statistics.median(v), "us": v, "compulsory_mb": round(moved[f] / 1e6, 1)}
+                         for f, v in res.items()}}), flush=True)
     return 0
 
 
@@ -1269,9 +1340,10 @@ def main() -> int:
     ap.add_argument("--window", choices=("global", "band"), default=None,
                     help="--compare: the layer's window (default: the workload's first layer)")
     ap.add_argument("--sets", type=int, default=4, help="--compare: distinct Q/K/V sets cycled over (default 4)")
-    ap.add_argument("--variant-timing", choices=("gate", "side-stream"), default=None,
+    ap.add_argument("--variant-timing", choices=("gate", "side-stream", "rope"), default=None,
                     help="only time one layer call of --workload in two forms, interleaved: with and without its "
-                         "gate, or a mixed batch's short pass on a second stream against one stream")
+                         "gate, a mixed batch's short pass on a second stream against one stream, or RoPE kernel + "
+                         "attention against the fused RoPE prologue (all-short workloads)")
     ap.add_argument("--graph-overhead", action="store_true",
                     help="only measure a HIP-graph replay's fixed and per-node cost against eager launches")
     ap.add_argument("--peaks", action="store_true",

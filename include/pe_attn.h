@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define PE_ATTN_ABI_VERSION 8
+#define PE_ATTN_ABI_VERSION 9
 
 #define PE_ATTN_OK 0
 #define PE_ATTN_EINVAL (-1)       /* malformed arguments (maps to ValueError) */
@@ -108,6 +108,21 @@ typedef struct pe_attn_args {
        tiled kernels, which serve any length, so a bound that is wrong costs time, never
        results. 0 <= min_seqlen <= max_seqlen. */
     int32_t min_seqlen;
+    /* Fused RoPE prologue (the reference's apply_rope_bshd before its attention,
+       packed_encoders/ops.py:485-499, _kernels/rope.py:302-349), or NULL for none. With
+       tables, q and k are the projection's unrotated rows (typically strided views into the
+       packed qkv) and the kernel applies split-half RoPE before the products: packed row r
+       (query token r, key token r) takes row r % rope_table_rows of cos and sin [rows, head_dim]
+       (bf16, rows rope_table_stride elements apart: per-token gathered tables, or the [S, D]
+       tables of a dense [B, S] batch), with pe_rope_qkv_fwd's rounding, so the result is bit
+       for bit that of pe_rope_qkv_fwd followed by the call on its q and k. Served by the short
+       kernel: a call with tables needs head_dim 64 or 128, no cu_seqlens_k, and every segment
+       within the routing boundary (max_seqlen <= the effective short_max), else
+       PE_ATTN_EUNSUPPORTED. */
+    const void *rope_cos;
+    const void *rope_sin;
+    int64_t rope_table_stride;
+    int32_t rope_table_rows;
 } pe_attn_args;
 
 /* ABI version of the loaded library; callers compare it with PE_ATTN_ABI_VERSION. */

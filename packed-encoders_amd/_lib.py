@@ -12,7 +12,7 @@ from pathlib import Path
 
 from ._build import LIBRARY
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 DTYPE_BF16 = 1
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, ESCRATCH = 0, -1, -2, -3, -4, -5
@@ -75,6 +75,10 @@ class AttnArgs(ctypes.Structure):
         ("max_seqlen_k", ctypes.c_int32),
         ("band_kernel", ctypes.c_int32),
         ("min_seqlen", ctypes.c_int32),
+        ("rope_cos", ctypes.c_void_p),
+        ("rope_sin", ctypes.c_void_p),
+        ("rope_table_stride", ctypes.c_int64),
+        ("rope_table_rows", ctypes.c_int32),
     ]
 
 

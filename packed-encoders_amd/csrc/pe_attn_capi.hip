@@ -85,6 +85,13 @@ int check_args(const pe_attn_args *a, bool need_pointers = true) {
     if (a->band_kernel < 0 || a->band_kernel > 2) return PE_ATTN_EINVAL;
     if (a->min_seqlen < 0 || a->min_seqlen > a->max_seqlen) return PE_ATTN_EINVAL;
     if (a->cu_seqlens_k && (a->total_tokens_k < 0 || a->max_seqlen_k < 0)) return PE_ATTN_EINVAL;
+    if (a->rope_cos || a->rope_sin) {
+        if (!a->rope_cos || !a->rope_sin || a->rope_table_rows < 1 || a->rope_table_stride < a->head_dim ||
+            (a->rope_table_stride & 7) || !aligned16(a->rope_cos) || !aligned16(a->rope_sin))
+            return PE_ATTN_EINVAL;
+        // The fused prologue lives in the short kernel (prepare() also needs every segment short).
+        if (a->head_dim > 128 || a->cu_seqlens_k) return PE_ATTN_EUNSUPPORTED;
+    }
     if (!need_pointers || a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
     if (!a->q || !a->k || !a->v || !a->o || !a->cu_seqlens) return PE_ATTN_EINVAL;
     const void *ptrs[4] = {a->q, a->k, a->v, a->o};
@@ -209,13 +216,20 @@ AttnParams make_params(const pe_attn_args *a, int short_max) {
     p.strip = effective_strip(a);
     p.band = uses_band64(a) ? 1 : 0;
     p.c = a->softmax_scale * pe::kLog2e;
+    p.rcos = static_cast<const __bf16 *>(a->rope_cos);
+    p.rsin = static_cast<const __bf16 *>(a->rope_sin);
+    p.rst = a->rope_table_stride;
+    p.rrows = a->rope_table_rows;
     return p;
 }
 
 template <int D, int SK, int HPW, bool GATE>
 int launch_short_t(const AttnParams &p, hipStream_t stream) {
     dim3 grid(p.n_seq, (p.hq + HPW - 1) / HPW);
-    hipLaunchKernelGGL((pe::short_attn_kernel<D, SK, HPW, GATE>), grid, dim3(256), 0, stream, p);
+    if (p.rcos)
+        hipLaunchKernelGGL((pe::short_attn_kernel<D, SK, HPW, GATE, true>), grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((pe::short_attn_kernel<D, SK, HPW, GATE, false>), grid, dim3(256), 0, stream, p);
     return hipGetLastError() == hipSuccess ? PE_ATTN_OK : PE_ATTN_ELAUNCH;
 }
 
@@ -363,6 +377,8 @@ int prepare(const pe_attn_args *a, Plan *plan) {
     int rc = check_args(a);
     if (rc) return rc;
     plan->sm = effective_short_max(a);
+    // RoPE tables: the fused prologue is the short kernel's, so no segment may reach a tiled one.
+    if (a->rope_cos && (plan->sm == 0 || a->max_seqlen > plan->sm)) return PE_ATTN_EUNSUPPORTED;
     plan->g = heads_per_tile(a);
     plan->bm = tile_rows(a, plan->g);
     plan->strip = effective_strip(a);

@@ -49,6 +49,9 @@ struct AttnParams {
     const int4 *work;          // tiled kernels: (segment, first q-tile, query start, query rows)
     const int32_t *work_count; // tiled kernels: number of valid entries
     int32_t work_cap;          // entries the workspace holds
+    const __bf16 *rcos, *rsin; // short kernel's fused RoPE tables [rows, D] (NULL: none)
+    int64_t rst;               // table row stride, elements
+    int32_t rrows;             // table rows: packed row r takes row r % rrows
 };
 
 // A tiled kernel's work item: the plan's (segment, first query tile, query start, query rows)

@@ -15,13 +15,22 @@
 // one launch of this kernel and one of the tiled kernel split a mixed batch per segment with
 // no host read of cu_seqlens. Global accesses go through buffer resources bounded by the
 // segment: rows past its end read as zero and are never written.
+//
+// ROPE: q and k are unrotated projection rows and the workgroup applies split-half RoPE itself
+// (pe_attn_args.rope_cos / rope_sin; rope8, the RoPE kernel's rounding). The table rows of the
+// wave's query rows and of the segment's keys are loaded with the other loads, before the one
+// wait. A lane's query fragment holds dims 16 c + 8 kg .. + 7 (c < D / 16), so both halves of
+// every rotation pair (c, c + D / 32) are already in its registers; the keys are rotated once
+// in LDS, each thread taking (key, 16-byte column pair) items of every head of the group,
+// behind one more barrier.
 #pragma once
 
 #include "pe_attn_stage.h"
+#include "pe_rope.h"
 
 namespace pe {
 
-template <int D, int SK, int HPW, bool GATE>
+template <int D, int SK, int HPW, bool GATE, bool ROPE>
 __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
     static_assert(SK % 32 == 0 && SK <= 128 && (4 % HPW) == 0, "short tile shape");
     constexpr int NB = SK / 32;
@@ -62,6 +71,22 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
 #pragma unroll
         for (int c = 0; c < DC; ++c) qf[i][c] = buf_ld16(q_rs, qoff + c * 32, 0);
     }
+    // ROPE: the table rows of those query rows, at the fragment's dims (packed row r takes
+    // table row r % rrows; rows past the segment are zero in qf, so their tables do not matter).
+    constexpr int QT = ROPE ? NQ : 1, CT = ROPE ? DC : 1;
+    bf16x8 qcos[QT][CT], qsin[QT][CT];
+    if constexpr (ROPE) {
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) {
+            const int64_t trow = ((int64_t)start + 32 * (wave / HPW + i * WSTEP) + col) % p.rrows;
+            const __bf16 *cr = p.rcos + trow * p.rst + kg * 8, *sr = p.rsin + trow * p.rst + kg * 8;
+#pragma unroll
+            for (int c = 0; c < DC; ++c) {
+                qcos[i][c] = ld_g16(cr + 16 * c);
+                qsin[i][c] = ld_g16(sr + 16 * c);
+            }
+        }
+    }
 
     // K and V of every head of the group: unit u = (j * 4 + wave) * 64 + lane of a tile holds
     // key u / CPR, global column (u % CPR) ^ swz(key); keys >= Lk read as zero.
@@ -83,8 +108,53 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
             dma16(dst + TILE * 2, key * v_row + ch * 16, v_rs);
         }
     }
+    // ROPE: the keys' table rows for this thread's (key, column pair) items: item it * 256 + tid
+    // is key / (CPR / 2) and column pair (j, j + CPR / 2), j = item % (CPR / 2).
+    constexpr int HALF = CPR / 2;
+    constexpr int KITEMS = ROPE ? (SK * HALF + 255) / 256 : 1;
+    bf16x8 kcos[KITEMS][2], ksin[KITEMS][2];
+    if constexpr (ROPE) {
+#pragma unroll
+        for (int it = 0; it < KITEMS; ++it) {
+            const int item = it * 256 + tid, key = item / HALF, j = item % HALF;
+            const int64_t trow = ((int64_t)kstart + key) % p.rrows;
+            const __bf16 *cr = p.rcos + trow * p.rst + 8 * j, *sr = p.rsin + trow * p.rst + 8 * j;
+            if (key < Lk) {
+                kcos[it][0] = ld_g16(cr);
+                kcos[it][1] = ld_g16(cr + D / 2);
+                ksin[it][0] = ld_g16(sr);
+                ksin[it][1] = ld_g16(sr + D / 2);
+            }
+        }
+    }
     wait_vmcnt<0>();
     __syncthreads();
+    if constexpr (ROPE) {
+        // Rotate every head's keys in place (column c of key r sits at unit c ^ swz(r) of its
+        // row), then let every wave see all of them.
+#pragma unroll
+        for (int it = 0; it < KITEMS; ++it) {
+            const int item = it * 256 + tid, key = item / HALF, j = item % HALF;
+            if (key >= Lk) continue;
+            const int lo_off = key * D + ((j ^ swz<CPR>(key)) * 8);
+            const int hi_off = key * D + (((j + HALF) ^ swz<CPR>(key)) * 8);
+#pragma unroll
+            for (int hs = 0; hs < HPW; ++hs) {
+                if (h0 + hs >= p.hq) break;
+                __bf16 *kt_hs = &kv[hs][0][0];
+                bf16x8 lo = ld_s16(kt_hs + lo_off), hi = ld_s16(kt_hs + hi_off);
+                rope8(lo, hi, kcos[it][0], kcos[it][1], ksin[it][0], ksin[it][1]);
+                *reinterpret_cast<bf16x8 *>(kt_hs + lo_off) = lo;
+                *reinterpret_cast<bf16x8 *>(kt_hs + hi_off) = hi;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NQ; ++i)
+#pragma unroll
+            for (int c = 0; c < DC / 2; ++c)
+                rope8(qf[i][c], qf[i][c + DC / 2], qcos[i][c], qcos[i][c + DC / 2], qsin[i][c], qsin[i][c + DC / 2]);
+    }
     if (!wave_head) return;
 
     // Per-lane LDS offsets: K key 32b + col, unit 2c + kg; V^T as in the tiled kernels.

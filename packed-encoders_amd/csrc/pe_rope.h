@@ -35,9 +35,25 @@ struct RopeParams {
     int32_t heads;
 };
 
+// Split-half RoPE of 8 elements of a head's low half (lo) and their high-half partners (hi),
+// in place, with the table elements of the same dims: each product rounded to fp32, then
+// summed (no fused multiply-add), then rounded to bf16. The attention kernels' fused prologue
+// uses the same function, so fused and separate RoPE agree bit for bit.
+__device__ __forceinline__ void rope8(bf16x8 &lo, bf16x8 &hi, const bf16x8 &cl, const bf16x8 &ch, const bf16x8 &sl,
+                                      const bf16x8 &sh) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float a = (float)lo[j], b = (float)hi[j];
+        const float l1 = a * (float)cl[j], l2 = b * (float)sl[j];
+        const float h1 = b * (float)ch[j], h2 = a * (float)sh[j];
+        lo[j] = (__bf16)(l1 - l2);
+        hi[j] = (__bf16)(h1 + h2);
+    }
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void rope_qkv_kernel(RopeParams p) {
-#pragma clang fp contract(off)
     constexpr int CH = D / 16;  // chunk pairs per head
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t per_row = 2LL * p.heads * CH;
@@ -53,18 +69,10 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(RopeParams p) {
     const int64_t trow = row % p.table_rows;
     const __bf16 *cs = p.cos + trow * p.table_st;
     const __bf16 *sn = p.sin + trow * p.table_st;
-    const bf16x8 xl = ld_g16(x + lo), xh = ld_g16(x + hi);
+    bf16x8 ol = ld_g16(x + lo), oh = ld_g16(x + hi);
     const bf16x8 cl = ld_g16(cs + lo), ch = ld_g16(cs + hi);
     const bf16x8 sl = ld_g16(sn + lo), sh = ld_g16(sn + hi);
-    bf16x8 ol, oh;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float a = (float)xl[j], b = (float)xh[j];
-        const float l1 = a * (float)cl[j], l2 = b * (float)sl[j];
-        const float h1 = b * (float)ch[j], h2 = a * (float)sh[j];
-        ol[j] = (__bf16)(l1 - l2);
-        oh[j] = (__bf16)(h1 + h2);
-    }
+    rope8(ol, oh, cl, ch, sl, sh);
     __bf16 *out = (which == 0 ? p.q_out : p.k_out) + (row * p.heads + h) * D;
     *reinterpret_cast<bf16x8 *>(out + lo) = ol;
     *reinterpret_cast<bf16x8 *>(out + hi) = oh;

@@ -132,11 +132,18 @@ def _attention_context(qkv: Tensor, kind: LayerKind, params: ModernBertParams, b
                        cu_seqlens: Tensor | None, max_seqlen: int | None) -> Tensor:
     """RoPE and attention over ``qkv [B, S, 3*H*D]``; returns the context ``[B, S, H*D]``.
     The HIP path rotates q and k straight out of ``qkv`` into contiguous ``[B, S, H, D]`` and
-    leaves v a strided view (token stride 3HD) that the kernels read in place; the dense path
-    splits and transposes to ``[B, H, S, D]``."""
+    leaves v a strided view (token stride 3HD) that the kernels read in place, or, with the
+    default pieces on short segments, lets the attention kernel rotate them itself
+    (``ops.flash_attention_qkv_bshd``); the dense path splits and transposes to
+    ``[B, H, S, D]``."""
     b, s = qkv.shape[:2]
     h, d = params.num_attention_heads, params.head_dim
     if ops.use_bshd_rope(backend, h, d, cu_seqlens):
+        if execution.rope_qkv is ops.rope_qkv and execution.attention_bshd is ops.attention_bshd:
+            # the default pieces: one call, with RoPE fused into the attention kernel when it fits
+            return ops.flash_attention_qkv_bshd(qkv, h, d, cos=kind.cos, sin=kind.sin, window=kind.window,
+                                                scaling=params.scaling, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen,
+                                                backend=backend)
         q, k = execution.rope_qkv(qkv, h, d, kind.cos, kind.sin)
         v = qkv.view(b, s, 3, h, d).select(2, 2)
         return execution.attention_bshd(q, k, v, window=kind.window, scaling=params.scaling,

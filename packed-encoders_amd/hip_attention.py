@@ -40,7 +40,8 @@ def _aligned(t: Tensor) -> Tensor:
 def _args(q: Tensor, k: Tensor, v: Tensor, o: Tensor, cu: Tensor, max_seqlen: int, scale: float,
           window_left: int, window_right: int, causal: bool, gate: Tensor | None,
           short_max: int, strip: int = 0, cu_k: Tensor | None = None,
-          max_seqlen_k: int = 0, band_kernel: int = 0, min_seqlen: int = 0) -> _lib.AttnArgs:
+          max_seqlen_k: int = 0, band_kernel: int = 0, min_seqlen: int = 0,
+          rope: tuple[Tensor, Tensor] | None = None) -> _lib.AttnArgs:
     a = _lib.AttnArgs()
     a.struct_size = ctypes.sizeof(_lib.AttnArgs)
     a.dtype = _lib.DTYPE_BF16
@@ -68,6 +69,10 @@ def _args(q: Tensor, k: Tensor, v: Tensor, o: Tensor, cu: Tensor, max_seqlen: in
         a.cu_seqlens_k = cu_k.data_ptr()
         a.total_tokens_k = k.shape[0]
         a.max_seqlen_k = int(max_seqlen_k)
+    if rope is not None:
+        cos, sin = rope
+        a.rope_cos, a.rope_sin = cos.data_ptr(), sin.data_ptr()
+        a.rope_table_stride, a.rope_table_rows = cos.stride(0), cos.shape[0]
     return a
 
 
@@ -131,20 +136,36 @@ def _plan_key(args: _lib.AttnArgs, cu: Tensor, cu_k: Tensor | None = None) -> tu
             args.strip, args.band_kernel, args.min_seqlen, *kv)
 
 
+def _table_rows(t: Tensor) -> Tensor:
+    """A RoPE table as [rows, D] with 16-byte rows (a copy only when its layout needs one)."""
+    return t if (t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and t.stride(0) % 8 == 0) else t.contiguous()
+
+
 def _varlen_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int,
                  softmax_scale: float, window_left: int, window_right: int, causal: bool,
                  gate: Tensor | None, short_max: int, cu_seqlens_k: Tensor | None = None,
-                 max_seqlen_k: int = 0, band_kernel: int = 0, min_seqlen: int = 0) -> Tensor:
+                 max_seqlen_k: int = 0, band_kernel: int = 0, min_seqlen: int = 0,
+                 rope_cos: Tensor | None = None, rope_sin: Tensor | None = None) -> Tensor:
     _check_tensors(q, k, v, cu_seqlens, gate, cu_seqlens_k)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     gate = _aligned(gate) if gate is not None else None
+    rope = None
+    if (rope_cos is None) != (rope_sin is None):
+        raise ValueError("RoPE needs both cos and sin tables")
+    if rope_cos is not None:
+        if rope_cos.dtype != _BF16 or rope_sin.dtype != _BF16 or rope_cos.device != q.device:
+            raise ValueError("RoPE tables must be bf16 on q's device")
+        rope_cos, rope_sin = _rope_tables(rope_cos, rope_sin, q.shape[2])
+        rope = (_table_rows(rope_cos), _table_rows(rope_sin))
+        if rope[0].stride(0) != rope[1].stride(0):
+            rope = (rope[0].contiguous(), rope[1].contiguous())
     out = torch.empty(q.shape, dtype=_BF16, device=q.device)
     if q.shape[0] == 0 or cu_seqlens.numel() < 2:
         return out
     lib = _lib.library()
     args = _args(q, k, v, out, cu_seqlens, max_seqlen, softmax_scale, window_left, window_right,
                  causal, gate, short_max, cu_k=cu_seqlens_k, max_seqlen_k=max_seqlen_k, band_kernel=band_kernel,
-                 min_seqlen=min_seqlen)
+                 min_seqlen=min_seqlen, rope=rope)
     stream = torch.cuda.current_stream(q.device).cuda_stream
     plans = _PLANS.get()
     if plans is None:
@@ -188,9 +209,11 @@ def _short_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen:
 
 def _varlen_op_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int, softmax_scale: float,
                     window_left: int, window_right: int, causal: bool, gate: Tensor | None, short_max: int,
-                    band_kernel: int = 0, min_seqlen: int = 0) -> Tensor:
+                    band_kernel: int = 0, min_seqlen: int = 0, rope_cos: Tensor | None = None,
+                    rope_sin: Tensor | None = None) -> Tensor:
     return _varlen_impl(q, k, v, cu_seqlens, max_seqlen, softmax_scale, window_left, window_right, causal, gate,
-                        short_max, band_kernel=band_kernel, min_seqlen=min_seqlen)
+                        short_max, band_kernel=band_kernel, min_seqlen=min_seqlen, rope_cos=rope_cos,
+                        rope_sin=rope_sin)
 
 
 def _varlen_kv_impl(q: Tensor, k: Tensor, v: Tensor, cu_seqlens_q: Tensor, cu_seqlens_k: Tensor,
@@ -251,7 +274,8 @@ def _register() -> None:
     try:
         lib.define("varlen_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, int max_seqlen, "
                    "float softmax_scale, int window_left, int window_right, bool causal, Tensor? gate, "
-                   "int short_max, int band_kernel=0, int min_seqlen=0) -> Tensor")
+                   "int short_max, int band_kernel=0, int min_seqlen=0, Tensor? rope_cos=None, "
+                   "Tensor? rope_sin=None) -> Tensor")
         lib.define("packed_short_attention(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, int max_seqlen, "
                    "float softmax_scale, int window_left, int window_right) -> Tensor")
         lib.define("rope_qkv(Tensor qkv, Tensor cos, Tensor sin, int h, int d) -> Tensor[]")
@@ -279,7 +303,7 @@ def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_se
                      causal: bool = False, gate: Tensor | None = None,
                      short_max: int | None = None, cu_seqlens_k: Tensor | None = None,
                      max_seqlen_k: int | None = None, band_kernel: int = 0,
-                     min_seqlen: int | None = None) -> Tensor:
+                     min_seqlen: int | None = None, rope: tuple[Tensor, Tensor] | None = None) -> Tensor:
     """Packed varlen attention: q ``[T, Hq, D]``, k/v ``[T, Hkv, D]`` bf16, int32 ``cu_seqlens``.
 
     ``window=(left, right)`` bounds ``i - j <= left`` and ``j - i <= right`` (-1 unbounded,
@@ -299,6 +323,14 @@ def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_se
     ``pe_attn_args.band_kernel``): 0 the library's choice by call size, 1 the streaming band
     kernel, 2 the tiled kernel; results agree within bf16 rounding, not bit for bit.
 
+    ``rope=(cos, sin)`` fuses the RoPE producer into the call: q and k are then the
+    projection's unrotated rows (e.g. strided views into ``qkv``), and each packed row ``r``
+    is rotated with row ``r % rows`` of the bf16 ``[rows, D]`` (or ``[1, rows, D]``) tables,
+    bit for bit as ``rope_qkv`` would (packed_encoders/ops.py:485-499,
+    _kernels/rope.py:302-349). The short kernel applies it, so every segment must be short
+    (``max_seqlen`` within the routing boundary; head_dim 64 or 128; no ``cu_seqlens_k``):
+    ``ValueError`` otherwise.
+
     ``min_seqlen`` is an optional host lower bound on the query segment lengths (a collator
     that packs host-known lengths has it beside ``max_seqlen``; None takes the enclosing
     ``shared_plans`` scope's bound, 0 outside one). When it exceeds the routing
@@ -317,6 +349,8 @@ def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_se
     if short_max is None:
         short_max = -1
     if cu_seqlens_k is not None:
+        if rope is not None:
+            raise ValueError("the fused RoPE prologue takes shared key segments (no cu_seqlens_k)")
         if max_seqlen_k is None:
             raise ValueError("cu_seqlens_k needs max_seqlen_k")
         return torch.ops.pe_hip.varlen_attention_kv(q, k, v, cu_seqlens, cu_seqlens_k, int(max_seqlen),
@@ -325,7 +359,8 @@ def varlen_attention(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_se
                                                     min_seqlen)
     return torch.ops.pe_hip.varlen_attention(q, k, v, cu_seqlens, int(max_seqlen), scale,
                                              int(window[0]), int(window[1]), bool(causal), gate,
-                                             int(short_max), int(band_kernel), min_seqlen)
+                                             int(short_max), int(band_kernel), min_seqlen,
+                                             *(rope if rope is not None else (None, None)))
 
 
 def packed_short_attention_supported(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor,

@@ -153,6 +153,45 @@ def attention_bshd(q: Tensor, k: Tensor, v: Tensor, *, window: tuple[int, int], 
     return out.reshape(b, s, h * d)
 
 
+def fused_rope_applies(qkv: Tensor, d: int, seq: int) -> bool:
+    """Whether ``flash_attention_qkv_bshd`` fuses RoPE into the attention call: bf16 on the
+    GPU, head_dim 64 or 128, and segments of at most 128 tokens, which the short kernel (the one
+    that carries the fused prologue) serves whole."""
+    return qkv.is_cuda and qkv.dtype == torch.bfloat16 and d in (64, 128) and 0 < seq <= 128
+
+
+def flash_attention_qkv_bshd(qkv: Tensor, h: int, d: int, *, cos: Tensor, sin: Tensor, window: tuple[int, int],
+                             scaling: float, cu_seqlens: Tensor | None = None, max_seqlen: int | None = None,
+                             backend: str = "hip") -> Tensor:
+    """RoPE + attention reading ``qkv [B, S, 3*h*d]`` directly (the reference's
+    ``flash_attention_qkv_bshd``, ops.py:485-499: its RoPE kernel, then ``attention_bshd``).
+    ``cos``/``sin`` are the ``rope_qkv`` tables. When every segment fits the short kernel
+    (``fused_rope_applies``) the RoPE is fused into the attention call: q and k are read
+    unrotated out of ``qkv`` and no rotated copy is written, with the same bits as the two
+    steps. Otherwise the RoPE kernel writes q and k and ``attention_bshd`` follows. Returns
+    ``[B, S, h*d]``."""
+    if backend != "hip":
+        raise ValueError(f"BSHD attention runs on the HIP kernels only (backend={backend!r})")
+    b, s = qkv.shape[:2]
+    view = qkv.view(b, s, 3, h, d)
+    if cu_seqlens is not None and b != 1:
+        raise ValueError("packed attention takes a batch of one flat sequence")
+    seq = s if cu_seqlens is None else int(max_seqlen)
+    if not fused_rope_applies(qkv, d, seq):
+        q, k = rope_qkv(qkv, h, d, cos, sin)
+        return attention_bshd(q, k, view[:, :, 2], window=window, scaling=scaling, cu_seqlens=cu_seqlens,
+                              max_seqlen=max_seqlen, backend=backend)
+    varlen_attention = _load_hip_attention()
+    floor = None  # packed: the enclosing shared_plans scope's host bound
+    if cu_seqlens is None:
+        cu_seqlens = torch.arange(0, (b + 1) * s, s, dtype=torch.int32, device=qkv.device)
+        max_seqlen = floor = s
+    q, k, v = (view[:, :, i].reshape(b * s, h, d) for i in range(3))
+    out = varlen_attention(q, k, v, cu_seqlens, int(max_seqlen), softmax_scale=scaling, window=tuple(window),
+                           min_seqlen=floor, rope=(cos.reshape(-1, d), sin.reshape(-1, d)))
+    return out.reshape(b, s, h * d)
+
+
 def attention(q: Tensor, k: Tensor, v: Tensor, *, mask: Tensor | None, window: tuple[int, int], scaling: float,
               backend: str, cu_seqlens: Tensor | None = None, max_seqlen: int | None = None) -> Tensor:
     """BHSD attention dispatch (ops.py:541-555): ``"sdpa"`` uses the additive ``mask``, ``"hip"``

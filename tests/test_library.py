@@ -69,7 +69,7 @@ def test_library_holds_gfx950_code():
 
 
 def test_abi_version_and_status_text(lib):
-    assert lib.pe_attn_abi_version() == 8
+    assert lib.pe_attn_abi_version() == 9
     assert lib.pe_attn_strerror(0) == b"ok"
     assert lib.pe_attn_strerror(-3) == b"workspace missing or too small"
     assert lib.pe_attn_strerror(-99) == b"unknown status"
