@@ -89,8 +89,10 @@ int check_args(const pe_attn_args *a, bool need_pointers = true) {
         if (!a->rope_cos || !a->rope_sin || a->rope_table_rows < 1 || a->rope_table_stride < a->head_dim ||
             (a->rope_table_stride & 7) || !aligned16(a->rope_cos) || !aligned16(a->rope_sin))
             return PE_ATTN_EINVAL;
-        // The fused prologue lives in the short kernel (prepare() also needs every segment short).
+        // The fused prologue lives in the short kernel (prepare() also needs every segment short),
+        // which reads the tables through a buffer resource with 32-bit offsets.
         if (a->head_dim > 128 || a->cu_seqlens_k) return PE_ATTN_EUNSUPPORTED;
+        if ((int64_t)a->rope_table_rows * a->rope_table_stride * 2 >= (int64_t)1 << 31) return PE_ATTN_EUNSUPPORTED;
     }
     if (!need_pointers || a->n_seq == 0 || a->total_tokens == 0) return PE_ATTN_OK;
     if (!a->q || !a->k || !a->v || !a->o || !a->cu_seqlens) return PE_ATTN_EINVAL;

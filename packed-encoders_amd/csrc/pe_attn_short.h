@@ -17,12 +17,12 @@
 // segment: rows past its end read as zero and are never written.
 //
 // ROPE: q and k are unrotated projection rows and the workgroup applies split-half RoPE itself
-// (pe_attn_args.rope_cos / rope_sin; rope8, the RoPE kernel's rounding). The table rows of the
-// wave's query rows and of the segment's keys are loaded with the other loads, before the one
-// wait. A lane's query fragment holds dims 16 c + 8 kg .. + 7 (c < D / 16), so both halves of
-// every rotation pair (c, c + D / 32) are already in its registers; the keys are rotated once
-// in LDS, each thread taking (key, 16-byte column pair) items of every head of the group,
-// behind one more barrier.
+// (pe_attn_args.rope_cos / rope_sin; rope8, the RoPE kernel's rounding). The segment's cos and
+// sin rows are staged in LDS with the K/V tiles (same loads, same swizzle, before the one
+// wait): the keys are then rotated once in LDS, each thread taking (key, 16-byte column pair)
+// items of every head of the group, behind one more barrier, and every wave rotates its query
+// fragment in registers (a lane's dims 16 c + 8 kg .. + 7, c < D / 16, hold both halves of every
+// rotation pair (c, c + D / 32)), reading the table values at the K operand's offsets.
 #pragma once
 
 #include "pe_attn_stage.h"
@@ -44,6 +44,9 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
     static_assert(UPT >= 1 && TILE % (8 * 256) == 0, "a tile must split into 1 KB wave loads");
 
     __shared__ __attribute__((aligned(16))) __bf16 kv[HPW][2][TILE];
+    // ROPE: the cos and sin rows of the segment's keys (= its query rows), laid out and
+    // swizzled as a K tile, so the key pass and the query fragments read them at K's offsets.
+    __shared__ __attribute__((aligned(16))) __bf16 tab[ROPE ? 2 : 1][ROPE ? TILE : 8];
 
     const int seg = blockIdx.x;
     const int start = p.cu[seg];
@@ -71,23 +74,6 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
 #pragma unroll
         for (int c = 0; c < DC; ++c) qf[i][c] = buf_ld16(q_rs, qoff + c * 32, 0);
     }
-    // ROPE: the table rows of those query rows, at the fragment's dims (packed row r takes
-    // table row r % rrows; rows past the segment are zero in qf, so their tables do not matter).
-    constexpr int QT = ROPE ? NQ : 1, CT = ROPE ? DC : 1;
-    bf16x8 qcos[QT][CT], qsin[QT][CT];
-    if constexpr (ROPE) {
-#pragma unroll
-        for (int i = 0; i < NQ; ++i) {
-            const int64_t trow = ((int64_t)start + 32 * (wave / HPW + i * WSTEP) + col) % p.rrows;
-            const __bf16 *cr = p.rcos + trow * p.rst + kg * 8, *sr = p.rsin + trow * p.rst + kg * 8;
-#pragma unroll
-            for (int c = 0; c < DC; ++c) {
-                qcos[i][c] = ld_g16(cr + 16 * c);
-                qsin[i][c] = ld_g16(sr + 16 * c);
-            }
-        }
-    }
-
     // K and V of every head of the group: unit u = (j * 4 + wave) * 64 + lane of a tile holds
     // key u / CPR, global column (u % CPR) ^ swz(key); keys >= Lk read as zero.
     const int k_row = (int)p.k_st * 2, v_row = (int)p.v_st * 2;
@@ -108,52 +94,63 @@ __global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
             dma16(dst + TILE * 2, key * v_row + ch * 16, v_rs);
         }
     }
-    // ROPE: the keys' table rows for this thread's (key, column pair) items: item it * 256 + tid
-    // is key / (CPR / 2) and column pair (j, j + CPR / 2), j = item % (CPR / 2).
-    constexpr int HALF = CPR / 2;
-    constexpr int KITEMS = ROPE ? (SK * HALF + 255) / 256 : 1;
-    bf16x8 kcos[KITEMS][2], ksin[KITEMS][2];
     if constexpr (ROPE) {
+        // Table rows of keys 0..SK-1 (row (kstart + key) % rrows), unit for unit as the K tile;
+        // keys past the segment take void loads (zeros, no traffic).
+        const uint32_t tbytes = (uint32_t)((int64_t)p.rrows * p.rst * 2);
+        const __amdgpu_buffer_rsrc_t c_rs = make_rsrc(p.rcos, tbytes), s_rs = make_rsrc(p.rsin, tbytes);
+        const uint32_t tab_base = uniform((int)lds_addr(&tab[0][0]));
 #pragma unroll
-        for (int it = 0; it < KITEMS; ++it) {
-            const int item = it * 256 + tid, key = item / HALF, j = item % HALF;
-            const int64_t trow = ((int64_t)kstart + key) % p.rrows;
-            const __bf16 *cr = p.rcos + trow * p.rst + 8 * j, *sr = p.rsin + trow * p.rst + 8 * j;
-            if (key < Lk) {
-                kcos[it][0] = ld_g16(cr);
-                kcos[it][1] = ld_g16(cr + D / 2);
-                ksin[it][0] = ld_g16(sr);
-                ksin[it][1] = ld_g16(sr + D / 2);
-            }
+        for (int j = 0; j < UPT; ++j) {
+            const int u = (j * 4 + wave) * 64 + lane;
+            const int key = u / CPR, ch = (u % CPR) ^ swz<CPR>(key);
+            const int row = (int)(((int64_t)kstart + key) % p.rrows);
+            const int off = key < Lk ? row * (int)p.rst * 2 + ch * 16 : kVoidOffset;
+            const uint32_t dst = (uint32_t)uniform((int)(tab_base + (uint32_t)((j * 4 + wave) * 1024)));
+            dma16(dst, off, c_rs);
+            dma16(dst + TILE * 2, off, s_rs);
         }
     }
     wait_vmcnt<0>();
     __syncthreads();
     if constexpr (ROPE) {
-        // Rotate every head's keys in place (column c of key r sits at unit c ^ swz(r) of its
-        // row), then let every wave see all of them.
+        // Rotate every head's keys in place, thread by (key, column pair (j, j + CPR / 2))
+        // items (column c of key r sits at unit c ^ swz(r) of its row, in the K tile and the
+        // tables alike), then let every wave see all of them.
+        constexpr int HALF = CPR / 2, ITEMS = (SK * HALF + 255) / 256;
 #pragma unroll
-        for (int it = 0; it < KITEMS; ++it) {
+        for (int it = 0; it < ITEMS; ++it) {
             const int item = it * 256 + tid, key = item / HALF, j = item % HALF;
             if (key >= Lk) continue;
             const int lo_off = key * D + ((j ^ swz<CPR>(key)) * 8);
             const int hi_off = key * D + (((j + HALF) ^ swz<CPR>(key)) * 8);
+            const bf16x8 cl = ld_s16(&tab[0][lo_off]), ch = ld_s16(&tab[0][hi_off]);
+            const bf16x8 sl = ld_s16(&tab[1][lo_off]), sh = ld_s16(&tab[1][hi_off]);
 #pragma unroll
             for (int hs = 0; hs < HPW; ++hs) {
                 if (h0 + hs >= p.hq) break;
                 __bf16 *kt_hs = &kv[hs][0][0];
                 bf16x8 lo = ld_s16(kt_hs + lo_off), hi = ld_s16(kt_hs + hi_off);
-                rope8(lo, hi, kcos[it][0], kcos[it][1], ksin[it][0], ksin[it][1]);
+                rope8(lo, hi, cl, ch, sl, sh);
                 *reinterpret_cast<bf16x8 *>(kt_hs + lo_off) = lo;
                 *reinterpret_cast<bf16x8 *>(kt_hs + hi_off) = hi;
             }
         }
         __syncthreads();
+        // The wave's query rows (row 32 qb + col) take the same tables: their fragment units
+        // 2 c + kg sit where the K operand's do (swz sees only the row's bits 0-3). Rows past
+        // the segment are zero in qf and in the tables.
 #pragma unroll
-        for (int i = 0; i < NQ; ++i)
+        for (int i = 0; i < NQ; ++i) {
+            const int rbase = 32 * (wave / HPW + i * WSTEP) * D + col * D;
 #pragma unroll
-            for (int c = 0; c < DC / 2; ++c)
-                rope8(qf[i][c], qf[i][c + DC / 2], qcos[i][c], qcos[i][c + DC / 2], qsin[i][c], qsin[i][c + DC / 2]);
+            for (int c = 0; c < DC / 2; ++c) {
+                const int lo_off = rbase + ((2 * c + kg) ^ swz<CPR>(col)) * 8;
+                const int hi_off = rbase + ((2 * (c + DC / 2) + kg) ^ swz<CPR>(col)) * 8;
+                rope8(qf[i][c], qf[i][c + DC / 2], ld_s16(&tab[0][lo_off]), ld_s16(&tab[0][hi_off]),
+                      ld_s16(&tab[1][lo_off]), ld_s16(&tab[1][hi_off]));
+            }
+        }
     }
     if (!wave_head) return;
 
