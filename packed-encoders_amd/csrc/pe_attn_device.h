@@ -156,6 +156,16 @@ __device__ __forceinline__ float sum2_first(const bf16x8 &p, int i) {
     return r;
 }
 
+// acc + p[2i] + p[2i + 1] in fp32 into a new register, acc kept: the VOP3P form of v_dot2 (the
+// accumulating VOP2 form would first copy acc with a separate move).
+__device__ __forceinline__ float sum2_from(const bf16x8 &p, int i, float acc) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 pair = {p[2 * i], p[2 * i + 1]};
+    float r;
+    asm("v_dot2_f32_bf16 %0, %1, %2, %3" : "=v"(r) : "v"(pair), "s"(0x3f803f80u), "v"(acc));
+    return r;
+}
+
 // Bits lo..hi (clamped to 0..31) of a 32-bit mask; 0 when the range is empty. lo >= 0.
 __device__ __forceinline__ uint32_t bit_range(int lo, int hi) {
     hi = min(hi, 31);

@@ -32,10 +32,11 @@
 // Softmax: online, fp32, log2 domain. The running maximum m of each row is only a reference
 // point shared by numerator and denominator: it is taken exactly on the query tile's first
 // 32-key block, and every later block reuses it with no max at all. A half
-// block whose probabilities under the stale m sum past 2^64 on some row is scored again
+// block that takes some row's probability sum under the stale m past 2^64 is scored again
 // exactly before its P.V product (m raised, accumulators rescaled), so no probability that
 // reaches the MFMAs can overflow. Probabilities are rounded to bf16 for P.V and the row sums
-// add exactly those bf16 values (v_dot2 with ones).
+// add exactly those bf16 values (v_dot2 with ones, continuing the row's sum, so that accepting
+// a half block is a register rename and its check one integer max and compare).
 //
 // Schedule of a full key tile (two 32-key blocks b0, b1) under the stale maximum, written so
 // that each wave's MFMA chain always has an independent VALU phase beside it:
@@ -58,7 +59,7 @@
 namespace pe {
 
 // log2 of the largest unnormalised probability the exact first tile lets stand before
-// rescaling, and the largest per-row probability sum of a half block accepted under a stale
+// rescaling, and the largest per-row probability sum a half block may leave under a stale
 // maximum (2^64).
 constexpr float kG64LazyRescale = 8.0f;
 constexpr float kG64OverflowGuard = 18446744073709551616.0f;
@@ -356,12 +357,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             m[x] = pair_max(fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]))) * c2;
             nm[x] = -m[x];
         };
-        // Softmax check of a half block: false when some row's probabilities pass the guard
-        // (nothing added), else its sums are added to the row sums.
+        // Probabilities of a half block under half x's stale m, computed in place, with the row
+        // sums continued from ls[x] into st0 / st1 (ls itself kept for the check below).
+        auto probs_onto = [&](f32x16 &s, int x, bf16x8 (&pb)[2], float &st0, float &st1) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s[j] = exp2_fast(fmaf(s[j], c2, nm[x]));
+            pb[0] = to_bf16x8(s, 0);
+            pb[1] = to_bf16x8(s, 8);
+            st0 = sum2_from(pb[0], 0, ls[x][0]);
+            st1 = sum2_from(pb[0], 1, ls[x][1]);
+            st0 = sum2(pb[0], 2, st0);
+            st1 = sum2(pb[0], 3, st1);
+            st0 = sum2(pb[1], 0, st0);
+            st1 = sum2(pb[1], 1, st1);
+            st0 = sum2(pb[1], 2, st0);
+            st1 = sum2(pb[1], 3, st1);
+        };
+        // Softmax check of a half block: false when some row's sums with it pass the guard
+        // (nothing taken: the exact path redoes the half block from ls), else they become the
+        // row sums. Sums of earlier accepted half blocks stay far below the guard unless a row's
+        // scores rose by ~60 log2 units, which the exact path then meets once and rescales. The
+        // sums are non-negative or NaN, so their bit patterns compare as integers in the order of
+        // their values (NaN above the guard): one integer max and compare, with none of the
+        // canonicalising moves a float max takes.
         auto accept = [&](int x, float st0, float st1) {
-            if (wave_any(fmaxf(st0, st1) > kG64OverflowGuard)) return false;
-            ls[x][0] += st0;
-            ls[x][1] += st1;
+            const int guard = __float_as_int(kG64OverflowGuard);
+            if (wave_any(max(__float_as_int(st0), __float_as_int(st1)) > guard)) return false;
+            ls[x][0] = st0;
+            ls[x][1] = st1;
             return true;
         };
         // A full key tile in the pipelined order, under the stale maximum. Returns 4 when done,
@@ -384,7 +407,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             if (first) seed_max(sa, 0);
             __builtin_amdgcn_sched_barrier(0);
             f32x16 sb = qk(k4, 1);
-            probs(sa, 0, pa, st0, st1);
+            probs_onto(sa, 0, pa, st0, st1);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -399,7 +422,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             load_v(vt, 0, v4);
             sa = qk(k4, 0);
             pv(v4, pa, 0);
-            probs(sb, 1, pbb, st0, st1);
+            probs_onto(sb, 1, pbb, st0, st1);
             __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
 #pragma unroll
@@ -413,7 +436,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             // R2: S_B1, O_B += V0 P_B0; softmax A1 under them.
             sb = qk(k4, 1);
             pv(v4, pbb, 1);
-            probs(sa, 0, pa, st0, st1);
+            probs_onto(sa, 0, pa, st0, st1);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -425,7 +448,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             // R3: O_A += V1 P_A1; softmax B1 under it.
             load_v(vt, 1, v4);
             pv(v4, pa, 0);
-            probs(sb, 1, pbb, st0, st1);
+            probs_onto(sb, 1, pbb, st0, st1);
             __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
 #pragma unroll
@@ -456,7 +479,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             if (first) seed_max(sa, 0);
             __builtin_amdgcn_sched_barrier(0);
             f32x16 sb = qk(k4, 1);
-            probs(sa, 0, pa, st0, st1);
+            probs_onto(sa, 0, pa, st0, st1);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -468,7 +491,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
             __builtin_amdgcn_sched_barrier(0);
             load_v(vt, b, v4);
             pv(v4, pa, 0);
-            probs(sb, 1, pbb, st0, st1);
+            probs_onto(sb, 1, pbb, st0, st1);
             __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
 #pragma unroll

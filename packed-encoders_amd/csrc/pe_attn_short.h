@@ -30,8 +30,17 @@
 
 namespace pe {
 
+// Waves per SIMD the compiler is asked to fit: a head_dim 64 workgroup of capacity 64 and at most
+// two heads takes 16 or 32 KB of LDS, so five fit a CU once its registers allow five waves per
+// SIMD (84 VGPRs instead of 105, no spills); the others are bound by LDS first.
+template <int D, int SK, int HPW, bool ROPE>
+constexpr int short_waves_per_eu() {
+    return D == 64 && SK == 64 && HPW <= 2 && !ROPE ? 5 : 1;
+}
+
 template <int D, int SK, int HPW, bool GATE, bool ROPE>
-__global__ __launch_bounds__(256) void short_attn_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(short_waves_per_eu<D, SK, HPW, ROPE>())))
+void short_attn_kernel(AttnParams p) {
     static_assert(SK % 32 == 0 && SK <= 128 && (4 % HPW) == 0, "short tile shape");
     constexpr int NB = SK / 32;
     constexpr int DC = D / 16;

@@ -663,6 +663,31 @@ def test_scores_jumping_past_a_stale_maximum(pe, jump, window, causal):
     _assert_parity(got, want, cu)
 
 
+def test_score_jump_in_a_tiles_last_half_block(pe):
+    """A jump that only the second 32 rows of each 64-row group see (their first 32 rows'
+    queries scaled down 64x), in the second 32-key block of a key tile (keys 224..255): only the
+    tile's last half block overflows the stale maximum. The global kernel runs that half block
+    under the next key tile's first products; here it is re-scored exactly there (segment of
+    700: tile 4 follows) and before a partial last key tile (segment of 300: tile 4 is partial),
+    and must match the oracle."""
+    lengths = [700, 300, 129]
+    announce("score jump in a tile's last half block")
+    q, k, v, cu, _ = _inputs(lengths, hq=4, seed=43)
+    q = q.float().abs()
+    k = k.float()
+    for a, n in ((0, 700), (700, 300), (1000, 129)):
+        rows = torch.arange(n)
+        q[a + rows[rows % 64 < 32]] /= 64.0
+    for a in (0, 700):
+        k[a + 224:a + 256] = 10.0
+    q, k = q.bfloat16(), k.bfloat16()
+    qd, kd, vd, cud = _dev(q, k, v, cu)
+    with torch.inference_mode():
+        got = pe.varlen_attention(qd, kd, vd, cud, max(lengths), softmax_scale=0.125, short_max=0)
+    want = _oracle(q, k, v, cu, scale=0.125)
+    _assert_parity(got, want, cu)
+
+
 @pytest.mark.parametrize("d,h", [(64, 12), (128, 6), (256, 8), (64, 1)])
 @pytest.mark.parametrize("tables", ["per-token", "dense-modulo", "batched"])
 def test_rope_qkv_is_bit_exact_against_the_oracle(pe, d, h, tables):
