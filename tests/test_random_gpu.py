@@ -17,6 +17,8 @@ call has a gate): the output was correctly rounded or off by the one step the bo
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -27,7 +29,10 @@ from oracle import attention as oa
 MAX_ABS = 2e-2
 MIN_COS = 0.9999
 HEADS = [(4, 4), (8, 2), (6, 3), (8, 8), (4, 1), (12, 12)]
-N_CASES = 96
+# Seeds [FIRST, FIRST + N_CASES): 96 from 0 by default; PE_RANDOM_FIRST / PE_RANDOM_CASES widen a
+# sweep without changing what a default run checks.
+FIRST = int(os.environ.get("PE_RANDOM_FIRST", "0"))
+N_CASES = int(os.environ.get("PE_RANDOM_CASES", "96"))
 
 
 def _lengths(rng, kind: str) -> list[int]:
@@ -151,7 +156,7 @@ def test_draws_cover_the_argument_space():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("seed", range(N_CASES))
+@pytest.mark.parametrize("seed", range(FIRST, FIRST + N_CASES))
 def test_random_call_matches_oracle(pe, seed):
     c = draw_case(seed)
     announce(f"random case {c}")
