@@ -92,3 +92,58 @@ def test_captured_call_replays_match_eager(pe, case):
             assert torch.isfinite(noise)
             assert torch.equal(got, want[:T]), f"{case}: replay with batch {i} differs from the eager call"
     del graph
+
+
+def test_captured_fused_rope_call_replays_match_eager(pe):
+    """varlen_attention(rope=(cos, sin)) on unrotated q/k views of a packed projection, captured
+    once: replays with the projection rows, the tables and cu_seqlens rewritten in place (five
+    segments of at most 64 tokens, 200 tokens, routed differently each time) equal the eager
+    call bit for bit."""
+    from oracle import rope
+
+    h, d, T = 12, 64, 200
+    batches = ([40, 64, 8, 56, 32], [64, 64, 64, 7, 1], [50, 50, 50, 25, 25])
+    assert all(sum(b) == T and len(b) == 5 for b in batches)
+    cos_np, sin_np = rope.rope_tables(4096, d, 10000.0)
+    g = torch.Generator(device="cuda").manual_seed(57)
+    rng = np.random.default_rng(57)
+
+    def draw():
+        pos = rng.integers(0, 4096, T)
+        return (torch.randn(T, 3 * h * d, device="cuda", generator=g, dtype=torch.bfloat16),
+                torch.from_numpy(cos_np[pos]).bfloat16().cuda(), torch.from_numpy(sin_np[pos]).bfloat16().cuda())
+
+    inputs = [draw() for _ in batches]
+    cus = [_cu(b) for b in batches]
+    qkv, cos, sin = (t.clone() for t in inputs[0])
+    cu = cus[0].clone()
+
+    def call(qkv, cos, sin, cu):
+        view = qkv.view(T, 3, h, d)
+        return pe.varlen_attention(view[:, 0], view[:, 1], view[:, 2], cu, 64, softmax_scale=0.125, rope=(cos, sin))
+
+    announce("graph capture fused rope: eager warm-up and capture")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.inference_mode():
+        with torch.cuda.stream(side):
+            call(qkv, cos, sin, cu)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = call(qkv, cos, sin, cu)
+        torch.cuda.synchronize()
+        for i in (0, 1, 2, 0, 2, 1):
+            announce(f"graph capture fused rope: replay with batch {i} {batches[i]}")
+            for dst, src in zip((qkv, cos, sin), inputs[i]):
+                dst.copy_(src)
+            cu.copy_(cus[i])
+            out.fill_(7.0)
+            graph.replay()
+            torch.cuda.synchronize()
+            got = out.clone()
+            want = call(*inputs[i], cus[i])
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"fused rope: replay with batch {i} differs from the eager call"
+    del graph

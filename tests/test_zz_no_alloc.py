@@ -110,6 +110,50 @@ def test_noalloc_matches_workspace_entry_point_on_random_calls(pe):
         assert torch.equal(outs[0], outs[1]), f"random case {seed}: noalloc output differs from the workspace entry point"
 
 
+@pytest.mark.parametrize("d,h", [(64, 12), (128, 6)], ids=["d64", "d128"])
+def test_noalloc_with_fused_rope_matches_workspace_entry_point(pe, d, h):
+    """The short kernel's fused RoPE (pe_attn_args.rope_cos / rope_sin, q and k unrotated views
+    of a packed projection) through the no-allocation entry point: the workspace entry point's
+    bits on two calls in a row, the second smaller, with the gate on the second."""
+    from oracle import rope
+
+    from packed_encoders_amd import _lib
+    from packed_encoders_amd.hip_attention import _args
+
+    lib = _lib.library()
+    stream = torch.cuda.current_stream().cuda_stream
+    cos_np, sin_np = rope.rope_tables(4096, d, 10000.0)
+    for call, (n_seq, gate) in enumerate(((300, False), (40, True))):
+        announce(f"noalloc fused rope d={d} call {call}: {n_seq} segments gate={gate}")
+        rng = np.random.default_rng(70 + call)
+        lengths = rng.integers(1, 65, size=n_seq).tolist()
+        T = sum(lengths)
+        g = torch.Generator().manual_seed(80 + call)
+        qkv = torch.randn(T, 3 * h * d, generator=g).bfloat16().cuda()
+        view = qkv.view(T, 3, h, d)
+        gt = torch.randn(T, h, d, generator=g).bfloat16().cuda() if gate else None
+        pos = rng.integers(0, 4096, T)
+        cos = torch.from_numpy(cos_np[pos]).bfloat16().cuda()
+        sin = torch.from_numpy(sin_np[pos]).bfloat16().cuda()
+        cu = torch.tensor([0, *np.cumsum(lengths).tolist()], dtype=torch.int32, device="cuda")
+        outs = []
+        for fn in ("workspace", "noalloc"):
+            out = torch.full((T, h, d), float("nan"), dtype=torch.bfloat16, device="cuda")
+            a = _args(view[:, 0], view[:, 1], view[:, 2], out, cu, max(lengths), d ** -0.5, -1, -1, False, gt, -1,
+                      rope=(cos, sin))
+            if fn == "noalloc":
+                assert lib.pe_varlen_attn_fwd_noalloc(ctypes.byref(a), stream) == 0
+            else:
+                size = ctypes.c_size_t()
+                assert lib.pe_attn_workspace_size(ctypes.byref(a), ctypes.byref(size)) == 0
+                ws = torch.empty(max(size.value, 1), dtype=torch.uint8, device="cuda")
+                assert lib.pe_varlen_attn_fwd(ctypes.byref(a), ws.data_ptr(), size.value, stream) == 0
+            torch.cuda.synchronize()
+            outs.append(out)
+        assert torch.isfinite(outs[1]).all(), "every output row is written"
+        assert torch.equal(outs[0], outs[1]), f"call {call}: noalloc output differs from the workspace entry point"
+
+
 def _inputs(T, hq, hkv, d, seed):
     g = torch.Generator().manual_seed(seed)
     return [torch.randn(T, h, d, generator=g).bfloat16().cuda() for h in (hq, hkv, hkv)]
