@@ -1357,7 +1357,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build runs one MI355X; "
-              "segments shard across GPUs with no exchange, see DESIGN.md", file=sys.stderr)
+              "packed segments would shard across GPUs by segment, with no exchange between them",
+              file=sys.stderr)
         return 2
 
     if args.profile_commands:
