@@ -35,6 +35,38 @@ def test_header_declares_the_expected_entry_points():
     assert _declared() == sorted(_lib.EXPORTED)
 
 
+@pytest.mark.parametrize("struct,cname", [("AttnArgs", "pe_attn_args"), ("RopeArgs", "pe_rope_args")])
+def test_ctypes_structs_match_the_header_layout(pe, tmp_path, struct, cname):
+    """Every field of the ctypes mirror sits at the offset, and has the size, that the C compiler
+    gives the header's struct (compiled on the host with gcc against include/pe_attn.h), and the
+    two structs have the same size: a field reordered or retyped on either side fails here, not
+    as a wrong argument on the GPU."""
+    import shutil
+
+    from packed_encoders_amd import _lib
+
+    gcc, hip_include = shutil.which("gcc"), "/opt/rocm/include"
+    if gcc is None or not (ROOT / "include").is_dir() or not __import__("os").path.isdir(hip_include):
+        pytest.skip("gcc or the HIP headers are not available")
+    cls = getattr(_lib, struct)
+    names = [f[0] for f in cls._fields_]
+    body = "".join(f'    printf("%s %zu %zu\\n", "{n}", offsetof({cname}, {n}), sizeof((({cname} *)0)->{n}));\n'
+                   for n in names)
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include "pe_attn.h"\nint main(void) {\n'
+                   f'    printf("sizeof %zu 0\\n", sizeof({cname}));\n{body}    return 0;\n}}\n')
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-D__HIP_PLATFORM_AMD__", "-I", str(ROOT / "include"), "-I", hip_include, str(src), "-o",
+                    str(exe)], check=True, capture_output=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        name, off, size = line.split()
+        got[name] = (int(off), int(size))
+    assert got.pop("sizeof")[0] == ctypes.sizeof(cls)
+    want = {n: (getattr(cls, n).offset, getattr(cls, n).size) for n in names}
+    assert got == want
+
+
 def test_library_exports_every_declared_symbol(lib):
     from packed_encoders_amd import _build
 
