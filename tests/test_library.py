@@ -67,6 +67,36 @@ def test_ctypes_structs_match_the_header_layout(pe, tmp_path, struct, cname):
     assert got == want
 
 
+def test_python_constants_match_the_header_macros(pe, tmp_path):
+    """The ABI version, dtype code, status codes, static scratch size and kernel codes that
+    _lib.py mirrors equal the header's macros, as the C compiler evaluates them."""
+    import os
+    import shutil
+
+    from packed_encoders_amd import _lib
+
+    gcc, hip_include = shutil.which("gcc"), "/opt/rocm/include"
+    if gcc is None or not os.path.isdir(hip_include):
+        pytest.skip("gcc or the HIP headers are not available")
+    mirror = {"ABI_VERSION": _lib.ABI_VERSION, "DTYPE_BF16": _lib.DTYPE_BF16, "OK": _lib.OK, "EINVAL": _lib.EINVAL,
+              "EUNSUPPORTED": _lib.EUNSUPPORTED, "EWORKSPACE": _lib.EWORKSPACE, "ELAUNCH": _lib.ELAUNCH,
+              "ESCRATCH": _lib.ESCRATCH, "STATIC_SCRATCH_BYTES": _lib.STATIC_SCRATCH_BYTES,
+              "KERNEL_NONE": _lib.KERNEL_NONE, "KERNEL_TILED": _lib.KERNEL_TILED,
+              "KERNEL_GLOBAL64": _lib.KERNEL_GLOBAL64, "KERNEL_BAND64": _lib.KERNEL_BAND64,
+              "KERNEL_WIDE": _lib.KERNEL_WIDE, "KERNEL_WIDE16": _lib.KERNEL_WIDE16}
+    declared = set(re.findall(r"^#define PE_ATTN_(\w+) ", HEADER.read_text(), flags=re.M))
+    assert set(mirror) <= declared, set(mirror) - declared
+    body = "".join(f'    printf("{n} %lld\\n", (long long)(PE_ATTN_{n}));\n' for n in mirror)
+    src = tmp_path / "macros.c"
+    src.write_text('#include <stdio.h>\n#include "pe_attn.h"\nint main(void) {\n' + body + "    return 0;\n}\n")
+    exe = tmp_path / "macros"
+    subprocess.run([gcc, "-D__HIP_PLATFORM_AMD__", "-I", str(ROOT / "include"), "-I", hip_include, str(src), "-o",
+                    str(exe)], check=True, capture_output=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    got = {n: int(v) for n, v in (line.split() for line in out.splitlines())}
+    assert got == mirror
+
+
 def test_library_exports_every_declared_symbol(lib):
     from packed_encoders_amd import _build
 
