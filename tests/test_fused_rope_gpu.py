@@ -135,3 +135,39 @@ def test_fused_rope_outside_the_short_kernel_is_refused(pe):
             varlen_attention(q256, q256, q256, cu, 200, rope=(c256, s256))
         with pytest.raises(ValueError):  # one table only
             varlen_attention(view[:, 0], view[:, 1], view[:, 2], cu, 200, rope=(cos, None))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_fused_rope_with_gqa(pe, d):
+    """Eight query heads on two kv heads, q / k / v as column views of one projection
+    [T, (8 + 2 + 2) * D]: the fused call equals, bit for bit, attention over q and k rotated by
+    the oracle (oracle/rope.rotate, the kernel's rounding: each product to fp32, their sum to
+    bf16) and uploaded, and matches the attention oracle at the reference's bar. Each query head
+    of a workgroup rotates its kv head's keys in its own LDS slot."""
+    from oracle import rope
+
+    from packed_encoders_amd.hip_attention import varlen_attention
+
+    hq, hkv = 8, 2
+    announce(f"fused rope gqa d={d}")
+    lengths = np.random.default_rng(d).integers(1, 65, size=60).tolist()
+    T = sum(lengths)
+    g = torch.Generator(device="cuda").manual_seed(d)
+    proj = torch.randn(T, (hq + 2 * hkv) * d, device="cuda", generator=g, dtype=torch.bfloat16)
+    q = proj[:, : hq * d].view(T, hq, d)
+    k = proj[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
+    v = proj[:, (hq + hkv) * d:].view(T, hkv, d)
+    cos, sin = _tables(T, d, seed=d + 1)
+    cu = torch.tensor([0, *np.cumsum(lengths).tolist()], dtype=torch.int32, device="cuda")
+    f = lambda t: t.float().cpu().numpy()
+    qr = rope.rotate(f(q), f(cos)[:, None, :], f(sin)[:, None, :])
+    kr = rope.rotate(f(k), f(cos)[:, None, :], f(sin)[:, None, :])
+    with torch.inference_mode():
+        got = varlen_attention(q, k, v, cu, max(lengths), softmax_scale=d ** -0.5, rope=(cos, sin))
+        two_step = varlen_attention(torch.from_numpy(qr).bfloat16().cuda(), torch.from_numpy(kr).bfloat16().cuda(),
+                                    v.contiguous(), cu, max(lengths), softmax_scale=d ** -0.5)
+    assert torch.equal(got, two_step)
+    want = oa.packed_attention(qr, kr, f(v), cu.cpu().numpy(), scale=d ** -0.5)
+    got64 = got.float().cpu().numpy().astype(np.float64)
+    assert np.abs(got64 - want).max() <= 2e-2
+    assert oa.cosine_per_token(got64, want).min() >= 0.9999
