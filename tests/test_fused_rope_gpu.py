@@ -40,7 +40,7 @@ SHAPES = [(64, 12, 32), (64, 12, 400), (64, 12, 700), (128, 6, 40), (128, 6, 700
 
 
 @pytest.mark.parametrize("d,h,n_seq", SHAPES, ids=[f"d{s[0]}_{s[2]}seg" for s in SHAPES])
-@pytest.mark.parametrize("tables", ["per-token", "dense-modulo"])
+@pytest.mark.parametrize("tables", ["per-token", "dense-modulo", "strided"])
 @pytest.mark.parametrize("window,gate", [((-1, -1), False), ((16, 16), True)], ids=["global", "band16-gate"])
 def test_fused_rope_is_bit_identical_to_rope_then_attention(pe, d, h, n_seq, tables, window, gate):
     from packed_encoders_amd.hip_attention import rope_qkv, varlen_attention
@@ -50,7 +50,10 @@ def test_fused_rope_is_bit_identical_to_rope_then_attention(pe, d, h, n_seq, tab
     lengths = rng.integers(1, 129 if n_seq < 100 else 65, size=n_seq).tolist()
     qkv, cu = _batch(lengths, h, d, seed=n_seq)
     T, max_len = sum(lengths), max(lengths)
-    cos, sin = _tables(T if tables == "per-token" else 97, d, seed=d)  # 97 rows: row r % 97
+    cos, sin = _tables(T if tables != "dense-modulo" else 97, d, seed=d)  # 97 rows: row r % 97
+    if tables == "strided":  # column views of one [T, 2 * D] table: row stride 2 * D
+        both = torch.cat([cos, sin], dim=1)
+        cos, sin = both[:, :d], both[:, d:]
     gt = torch.randn(T, h, d, device="cuda", dtype=torch.bfloat16) if gate else None
     view = qkv.view(T, 3, h, d)
     with torch.inference_mode():
