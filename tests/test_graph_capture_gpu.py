@@ -147,3 +147,46 @@ def test_captured_fused_rope_call_replays_match_eager(pe):
             torch.cuda.synchronize()
             assert torch.equal(got, want), f"fused rope: replay with batch {i} differs from the eager call"
     del graph
+
+
+def test_calls_on_two_streams_at_once_match_calls_alone(pe):
+    """Two streams issue calls back to back with no ordering between them (a short + global batch
+    on one, a +-64 batch with a gate on the other, each with its own workspace from the caching
+    allocator): every output equals the same call made alone on the default stream. The library
+    keeps no state between calls beyond the caller's workspace."""
+    g = torch.Generator(device="cuda").manual_seed(71)
+
+    def batch(lengths, h, d, gate):
+        T = sum(lengths)
+        q, k, v = (torch.randn(T, h, d, device="cuda", generator=g, dtype=torch.bfloat16) for _ in range(3))
+        gt = torch.randn(T, h, d, device="cuda", generator=g, dtype=torch.bfloat16) if gate else None
+        return q, k, v, gt, _cu(lengths), max(lengths)
+
+    a = batch([700, 40, 900, 30, 64, 1200], 12, 64, False)
+    b = batch([300, 1000, 77, 512], 8, 64, True)
+
+    def call_a(x):
+        q, k, v, gt, cu, mx = x
+        return pe.varlen_attention(q, k, v, cu, mx, softmax_scale=0.125)
+
+    def call_b(x):
+        q, k, v, gt, cu, mx = x
+        return pe.varlen_attention(q, k, v, cu, mx, softmax_scale=0.125, window=(64, 64), gate=gt)
+
+    announce("two streams: calls alone")
+    with torch.inference_mode():
+        want_a, want_b = call_a(a), call_b(b)
+        torch.cuda.synchronize()
+        s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+        s1.wait_stream(torch.cuda.current_stream())
+        s2.wait_stream(torch.cuda.current_stream())
+        outs_a, outs_b = [], []
+        announce("two streams: interleaved calls")
+        for _ in range(8):
+            with torch.cuda.stream(s1):
+                outs_a.append(call_a(a))
+            with torch.cuda.stream(s2):
+                outs_b.append(call_b(b))
+        torch.cuda.synchronize()
+    assert all(torch.equal(o, want_a) for o in outs_a), "a call on stream 1 differs from the call alone"
+    assert all(torch.equal(o, want_b) for o in outs_b), "a call on stream 2 differs from the call alone"
