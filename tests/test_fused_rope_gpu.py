@@ -174,3 +174,55 @@ def test_fused_rope_with_gqa(pe, d):
     got64 = got.float().cpu().numpy().astype(np.float64)
     assert np.abs(got64 - want).max() <= 2e-2
     assert oa.cosine_per_token(got64, want).min() >= 0.9999
+
+
+def _draw_rope_case(seed: int) -> dict:
+    rng = np.random.default_rng(1000 + seed)
+    d = int(rng.choice([64, 128]))
+    hq, hkv = [(12, 12), (8, 2), (6, 3), (4, 4), (4, 1)][int(rng.integers(0, 5))]
+    cap = int(rng.choice([32, 64, 128]))
+    lengths = rng.integers(1, cap + 1, size=int(rng.integers(1, 80))).tolist()
+    window = [(-1, -1), (16, 16), (0, 40), (33, 7)][int(rng.integers(0, 4))]
+    return dict(d=d, hq=hq, hkv=hkv, lengths=lengths, window=window, gate=bool(rng.integers(0, 2)),
+                tables=["per-token", "modulo", "strided"][int(rng.integers(0, 3))], seed=seed)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_fused_rope_calls(pe, seed):
+    """Seeded random fused-RoPE calls (head_dim 64 / 128, MHA and GQA, capacities 32 / 64 / 128,
+    windows, the gate, per-token, modulo and strided tables; q / k / v column views of one
+    projection): each equals, bit for bit, attention over q and k rotated by the oracle and
+    uploaded."""
+    from oracle import rope
+
+    from packed_encoders_amd.hip_attention import varlen_attention
+
+    c = _draw_rope_case(seed)
+    d, hq, hkv, lengths = c["d"], c["hq"], c["hkv"], c["lengths"]
+    announce(f"random fused rope {seed}: d={d} heads={hq}/{hkv} n={len(lengths)} max={max(lengths)} "
+             f"window={c['window']} gate={c['gate']} tables={c['tables']}")
+    T = sum(lengths)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    proj = torch.randn(T, (hq + 2 * hkv) * d, device="cuda", generator=g, dtype=torch.bfloat16)
+    q = proj[:, : hq * d].view(T, hq, d)
+    k = proj[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
+    v = proj[:, (hq + hkv) * d:].view(T, hkv, d)
+    gt = torch.randn(T, hq, d, device="cuda", generator=g, dtype=torch.bfloat16) if c["gate"] else None
+    rows = 53 if c["tables"] == "modulo" else T
+    cos, sin = _tables(rows, d, seed=seed + 7)
+    if c["tables"] == "strided":
+        both = torch.cat([cos, sin], dim=1)
+        cos, sin = both[:, :d], both[:, d:]
+    cu = torch.tensor([0, *np.cumsum(lengths).tolist()], dtype=torch.int32, device="cuda")
+    f = lambda t: t.float().cpu().numpy()
+    idx = np.arange(T) % rows
+    cr, sr = f(cos)[idx][:, None, :], f(sin)[idx][:, None, :]
+    qr = torch.from_numpy(rope.rotate(f(q), cr, sr)).bfloat16().cuda()
+    kr = torch.from_numpy(rope.rotate(f(k), cr, sr)).bfloat16().cuda()
+    with torch.inference_mode():
+        got = varlen_attention(q, k, v, cu, max(lengths), softmax_scale=d ** -0.5, window=c["window"], gate=gt,
+                               rope=(cos, sin))
+        want = varlen_attention(qr, kr, v.contiguous(), cu, max(lengths), softmax_scale=d ** -0.5,
+                                window=c["window"], gate=gt)
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, want), f"random fused rope case {seed} differs from attention over rotated q, k"
