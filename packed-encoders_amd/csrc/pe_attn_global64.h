@@ -203,7 +203,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     // A step's loads are complete once at most the following step's LPS loads are in flight
     // (loads complete in issue order; outstanding output stores only make the wait stricter),
     // or none when no following step was staged: the strip's last step leaves no load in
-    // flight, so the workgroup ends without draining its output stores.
+    // flight, so the workgroup ends without draining its output stores. Exact for NS = 3, where at
+    // most one following step is in flight; a deeper ring would need a wait sized by the steps
+    // actually in flight.
     int stage = 0;
     auto begin_step = [&]() {
         if (n_issued > n_begun + 1) wait_vmcnt<(NS - 2) * LPS>();

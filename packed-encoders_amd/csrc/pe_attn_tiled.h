@@ -254,7 +254,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void t
     // stricter), or none when no later step was staged, so the strip's last step leaves no load
     // in flight and the workgroup ends without draining its output stores. After the barrier
     // every wave is done with the previous step's stage, which is refilled with the step NS - 1
-    // ahead.
+    // ahead. The two cases are exact only for NS = 3 (at most one later step in flight): a deeper
+    // ring can have fewer than NS - 2 later steps in flight near a strip's end, and would need a
+    // wait sized by n_issued - n_begun - 1 instead (as the wide kernels take).
     auto begin_step = [&]() {
         if (n_issued > n_begun + 1) wait_vmcnt<(NS - 2) * LPS>();
         else wait_vmcnt<0>();
