@@ -54,7 +54,9 @@ typedef struct pe_attn_args {
     const void *q;        /* [total_tokens, n_heads_q,  head_dim] */
     const void *k;        /* [total_tokens, n_heads_kv, head_dim] */
     const void *v;        /* [total_tokens, n_heads_kv, head_dim] */
-    void *o;              /* [total_tokens, n_heads_q,  head_dim] (written) */
+    void *o;              /* [total_tokens, n_heads_q,  head_dim] (written); must not overlap q, k,
+                             v, gate or the RoPE tables: workgroups write o while others still
+                             read the inputs of their own rows' segment */
     const void *gate;     /* optional [total_tokens, n_heads_q, head_dim]; NULL for none */
     const int32_t *cu_seqlens; /* device [n_seq + 1] */
     /* strides in elements; the head_dim stride is 1. 16-byte alignment of every row is
